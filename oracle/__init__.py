@@ -1,0 +1,233 @@
+"""CPU oracle for the BFV NTT / keyswitch / share-GEMM path (ctypes over liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` and
+by the cpu_baseline leg of ``bench.py``, and there only as the checker.  The
+product package never imports it.
+
+The C restatement lives in ``oracle.c`` (each function cites the reference
+file:line it follows).  ``build()`` compiles it with the committed Makefile.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+u64p = ctypes.POINTER(ctypes.c_uint64)
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        vp, sz, u64, i32, u32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int, ctypes.c_uint32
+        sig = {
+            "orc_splitmix64": (u64, [u64, u64]),
+            "orc_fill_residues": (None, [vp, sz, sz, vp, sz, u64]),
+            "orc_fill_u64": (None, [vp, sz, u64]),
+            "orc_fill_i8": (None, [vp, sz, u64]),
+            "orc_fill_shift": (None, [vp, sz, u64]),
+            "orc_mulmod": (u64, [u64, u64, u64]),
+            "orc_powmod": (u64, [u64, u64, u64]),
+            "orc_invmod": (u64, [u64, u64]),
+            "orc_is_prime": (i32, [u64]),
+            "orc_gen_primes": (sz, [i32, u64, sz, vp]),
+            "orc_minimal_root": (u64, [u64, u64]),
+            "orc_shoup_quotient": (u64, [u64, u64]),
+            "orc_ntt_tables": (i32, [u64, ctypes.c_uint, vp, vp, vp]),
+            "orc_mul_shoup": (u64, [u64, u64, u64, u64]),
+            "orc_mul_barrett": (u64, [u64, u64, u64]),
+            "orc_ntt_forward": (None, [vp, ctypes.c_uint, u64, vp]),
+            "orc_ntt_inverse": (None, [vp, ctypes.c_uint, u64, vp, vp]),
+            "orc_ntt_batch": (None, [vp, sz, ctypes.c_uint, sz, vp, vp, vp, vp, i32, i32]),
+            "orc_galois": (None, [vp, vp, ctypes.c_uint, u64, u32]),
+            "orc_monomial_shift": (None, [vp, vp, ctypes.c_uint, u64, sz]),
+            "orc_keyswitch": (i32, [vp, vp, vp, sz, sz, vp, sz, sz, ctypes.c_uint, u32, vp, vp, vp, i32]),
+            "orc_share_gemm": (i32, [vp, vp, i32, vp, vp, sz, sz, sz, i32, i32]),
+            "orc_lift59": (u64, [u64, u64]),
+            "orc_dyadic_mac": (None, [vp, vp, vp, sz, sz, sz, sz, vp, sz]),
+            "orc_local_dot_scale": (None, [vp, vp, sz, sz, vp, u64, vp, sz, vp]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _u64(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint64))
+
+
+# ---------------------------------------------------------------- generators
+def fill_residues(limbs: int, n: int, q, seed: int) -> np.ndarray:
+    q = _u64(q)
+    out = np.empty((limbs, n), dtype=np.uint64)
+    lib().orc_fill_residues(_p(out), limbs, n, _p(q), len(q), seed)
+    return out
+
+
+def fill_u64(count: int, seed: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.uint64)
+    lib().orc_fill_u64(_p(out), count, seed)
+    return out
+
+
+def fill_i8(count: int, seed: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.int8)
+    lib().orc_fill_i8(_p(out), count, seed)
+    return out
+
+
+def fill_shift(count: int, seed: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.int8)
+    lib().orc_fill_shift(_p(out), count, seed)
+    return out
+
+
+# ------------------------------------------------------------- number theory
+def gen_primes(bits: int, n: int, count: int) -> list[int]:
+    """Largest primes below 2^bits congruent to 1 mod 2n, ascending (SEAL order)."""
+    out = np.zeros(count, dtype=np.uint64)
+    found = lib().orc_gen_primes(bits, 2 * n, count, _p(out))
+    assert found == count
+    return sorted(int(v) for v in out)
+
+
+def minimal_root(q: int, n: int) -> int:
+    return int(lib().orc_minimal_root(q, 2 * n))
+
+
+def ntt_tables(q: int, log_n: int):
+    n = 1 << log_n
+    fwd = np.zeros((n, 2), dtype=np.uint64)
+    inv = np.zeros((n, 2), dtype=np.uint64)
+    invn = np.zeros(2, dtype=np.uint64)
+    rc = lib().orc_ntt_tables(q, log_n, _p(fwd), _p(inv), _p(invn))
+    if rc:
+        raise ValueError("q is not 1 mod 2N")
+    return fwd, inv, invn
+
+
+class Tables:
+    """Stacked [primes][N][2] tables for a prime list."""
+
+    def __init__(self, q, log_n: int):
+        self.q = _u64(q)
+        self.log_n = log_n
+        f, i, n = zip(*(ntt_tables(int(x), log_n) for x in self.q))
+        self.fwd = np.ascontiguousarray(np.stack(f))
+        self.inv = np.ascontiguousarray(np.stack(i))
+        self.invn = np.ascontiguousarray(np.stack(n))
+
+
+# ----------------------------------------------------------------------- NTT
+def ntt(data: np.ndarray, tables: Tables, inverse: bool = False, threads: int = 0) -> np.ndarray:
+    """Batched transform of a [..][N] buffer whose limb l uses prime l % P (copy)."""
+    n = 1 << tables.log_n
+    out = np.array(data, dtype=np.uint64, copy=True, order="C")
+    limbs = out.size // n
+    lib().orc_ntt_batch(_p(out), limbs, tables.log_n, len(tables.q), _p(tables.q), _p(tables.fwd),
+                        _p(tables.inv), _p(tables.invn), int(inverse), threads)
+    return out
+
+
+def galois(poly: np.ndarray, q: int, log_n: int, g: int) -> np.ndarray:
+    src = _u64(poly)
+    out = np.empty_like(src)
+    lib().orc_galois(_p(src), _p(out), log_n, q, g)
+    return out
+
+
+def monomial_shift(poly: np.ndarray, q: int, log_n: int, e: int) -> np.ndarray:
+    src = _u64(poly)
+    out = np.empty_like(src)
+    lib().orc_monomial_shift(_p(src), _p(out), log_n, q, e)
+    return out
+
+
+# ----------------------------------------------------------------- keyswitch
+def keyswitch(ct: np.ndarray, key: np.ndarray, q, dnum: int, log_n: int, galois_elt: int = 1,
+              tables: Tables | None = None, per_ct_keys: bool = False, threads: int = 0) -> np.ndarray:
+    """ct [batch][2][L][N] coefficient form; key [dnum][2][L+1][N] (or
+    [batch][dnum][2][L+1][N] with per_ct_keys) NTT form; q has L+1 primes."""
+    q = _u64(q)
+    L = len(q) - 1
+    n = 1 << log_n
+    ct = _u64(ct)
+    key = _u64(key)
+    batch = ct.size // (2 * L * n)
+    if tables is None:
+        tables = Tables(q, log_n)
+    out = np.empty_like(ct)
+    stride = dnum * 2 * (L + 1) * n if per_ct_keys else 0
+    rc = lib().orc_keyswitch(_p(ct), _p(out), _p(key), stride, batch, _p(q), L, dnum, log_n, galois_elt,
+                             _p(tables.fwd), _p(tables.inv), _p(tables.invn), threads)
+    if rc:
+        raise ValueError(f"orc_keyswitch failed ({rc})")
+    return out
+
+
+# ---------------------------------------------------------------------- GEMM
+def share_gemm(x: np.ndarray, w: np.ndarray, shifts: np.ndarray | None = None, mask_bits: int = 64,
+               threads: int = 0) -> np.ndarray:
+    x = _u64(x)
+    w = np.ascontiguousarray(w)
+    assert w.dtype in (np.int8, np.int32)
+    m, k = x.shape
+    n, k2 = w.shape
+    assert k == k2
+    y = np.empty((m, n), dtype=np.uint64)
+    sh = None if shifts is None else np.ascontiguousarray(shifts, dtype=np.int8)
+    rc = lib().orc_share_gemm(_p(x), _p(w), 8 if w.dtype == np.int8 else 32, _p(sh), _p(y), m, k, n,
+                              mask_bits, threads)
+    assert rc == 0
+    return y
+
+
+def lift59(v: int, q: int) -> int:
+    return int(lib().orc_lift59(v, q))
+
+
+def local_dot_scale(shares: np.ndarray, weights: np.ndarray, delta, r: int, q) -> np.ndarray:
+    shares = _u64(shares)
+    weights = _u64(weights)
+    slots, words = shares.shape
+    q = _u64(q)
+    delta = _u64(delta)
+    out = np.empty((slots, len(q)), dtype=np.uint64)
+    lib().orc_local_dot_scale(_p(shares), _p(weights), words, slots, _p(delta), r, _p(q), len(q), _p(out))
+    return out
+
+
+def dyadic_mac(a: np.ndarray, w: np.ndarray, q) -> np.ndarray:
+    """a [blocks][limbs][N], w [blocks][wl][N] (limb l uses w limb l % wl, prime l % P)."""
+    a = _u64(a)
+    w = _u64(w)
+    q = _u64(q)
+    blocks, limbs, n = a.shape
+    wl = w.shape[1]
+    out = np.empty((limbs, n), dtype=np.uint64)
+    lib().orc_dyadic_mac(_p(a), _p(w), _p(out), blocks, limbs, n, len(q), _p(q), wl)
+    return out

@@ -1,0 +1,264 @@
+"""Pins the CPU oracle (oracle/oracle.c) against closed forms and fixtures.
+
+Nothing here retypes the oracle's butterfly or limb formulas: the checks are
+direct evaluation of the transform, big-integer CRT arithmetic, decryption
+invariants and the committed fixtures written from tests/golden/closed_form.py.
+"""
+import json
+import os
+import random
+
+import numpy as np
+import pytest
+
+import closed_form as cf
+import oracle
+
+MASK64 = (1 << 64) - 1
+
+
+@pytest.fixture(scope="module")
+def primes(golden_dir):
+    with open(os.path.join(golden_dir, "primes.json")) as f:
+        return json.load(f)
+
+
+def test_locked_primes_and_q(primes):
+    locked = [int(x) for x in primes["locked_primes"]]
+    assert locked == cf.LOCKED_PRIMES
+    # SEAL CoeffModulus::Create(16384, {60 x7}) rule (bfv.cpp:94-95)
+    assert oracle.gen_primes(60, 16384, 7) == locked
+    Qk = 1
+    for q in locked:
+        assert cf.is_prime(q) and q % 32768 == 1
+        Qk *= q
+    assert Qk == int(primes["Q_key_level"])
+    assert Qk // locked[6] == int(primes["Q_data_level"])
+    for name, vals in primes["sets"].items():
+        bits = {"locked_16384": 60, "c1_54bit_4096": 54, "c2_50bit_16384": 50, "c3_special_60bit_16384": 60}[name]
+        n = 4096 if "4096" in name else 16384
+        want = [int(v) for v in vals]
+        assert oracle.gen_primes(bits, n, len(want)) == want
+
+
+def test_minimal_root_matches_closed_form(primes):
+    psis = [int(x) for x in primes["psi_16384"]]
+    # values independently listed for the 7 locked primes
+    assert psis[:3] == [92056553354496, 27543819356734, 52069629205452]
+    for q, psi in zip(cf.LOCKED_PRIMES, psis):
+        assert oracle.minimal_root(q, 16384) == psi
+        assert pow(psi, 16384, q) == q - 1
+    for n in (2, 8, 64, 1024):
+        q = cf.primes_below(50, n, 1)[0]
+        assert oracle.minimal_root(q, n) == cf.minimal_psi(q, n)
+
+
+@pytest.mark.parametrize("log_n", [3, 6, 10, 14])
+def test_tables_closed_form(log_n):
+    n = 1 << log_n
+    for q in (cf.LOCKED_PRIMES[0], cf.LOCKED_PRIMES[6], cf.primes_below(50, max(n, 2), 1)[0]):
+        fwd, inv, invn = oracle.ntt_tables(q, log_n)
+        psi = oracle.minimal_root(q, n)
+        rng = random.Random(log_n)
+        for i in [1, 2, n - 1] + [rng.randrange(1, n) for _ in range(20)]:
+            if i >= n:
+                continue
+            assert int(fwd[cf.bitrev(i, log_n), 0]) == pow(psi, i, q)
+            assert int(inv[cf.bitrev(i - 1, log_n) + 1, 0]) == pow(psi, -i, q)
+        assert int(fwd[0, 0]) == 1 and int(inv[0, 0]) == 1
+        assert int(invn[0]) * n % q == 1
+        for tab in (fwd, inv):
+            for i in (0, 1, n // 2, n - 1):
+                w, wq = int(tab[i, 0]), int(tab[i, 1])
+                assert wq == (w << 64) // q
+
+
+def test_ntt_small_fixture(golden_dir):
+    data = np.load(os.path.join(golden_dir, "ntt_small.npz"))
+    names = sorted({k.rsplit("_", 1)[0] for k in data.files})
+    assert len(names) >= 12
+    for name in names:
+        q = int(data[name + "_q"][0])
+        a, want = data[name + "_in"], data[name + "_out"]
+        log_n = a.size.bit_length() - 1
+        t = oracle.Tables([q], log_n)
+        got = oracle.ntt(a[None, :], t)[0]
+        np.testing.assert_array_equal(got, want, err_msg=name)
+        back = oracle.ntt(got[None, :], t, inverse=True)[0]
+        np.testing.assert_array_equal(back, a, err_msg=name)
+
+
+def test_ntt_sampled_full_size(golden_dir):
+    with open(os.path.join(golden_dir, "ntt_sampled.json")) as f:
+        cases = json.load(f)
+    assert len(cases) == 15
+    import hashlib
+    for case in cases:
+        q, log_n, seed = int(case["q"]), case["log_n"], int(case["seed"])
+        n = 1 << log_n
+        a = oracle.fill_residues(1, n, [q], seed)
+        assert hashlib.sha256(a.tobytes()).hexdigest() == case["input_sha256"]
+        t = oracle.Tables([q], log_n)
+        out = oracle.ntt(a, t)[0]
+        for k, e in zip(case["k"], case["expected"]):
+            assert int(out[k]) == int(e), (case["set"], q, k)
+        assert np.array_equal(oracle.ntt(out[None], t, inverse=True)[0], a[0])
+
+
+def test_generator_matches_closed_form():
+    q = [cf.LOCKED_PRIMES[1], cf.LOCKED_PRIMES[4]]
+    got = oracle.fill_residues(3, 16, q, 12345)
+    want = cf.residues(12345, 3, 16, q)
+    assert got.tolist() == want
+    assert oracle.fill_u64(5, 7).tolist() == [cf.splitmix64(7, i) for i in range(5)]
+    i8 = oracle.fill_i8(1000, 99)
+    assert i8.min() >= -127 and i8.max() <= 127
+    assert i8.tolist()[:4] == [((cf.splitmix64(99, i) * 255) >> 64) - 127 for i in range(4)]
+
+
+def test_negacyclic_convolution_via_ntt():
+    log_n = 6
+    n = 1 << log_n
+    for q in (cf.LOCKED_PRIMES[2], cf.primes_below(50, n, 1)[0]):
+        t = oracle.Tables([q], log_n)
+        a = oracle.fill_residues(1, n, [q], 1)
+        b = oracle.fill_residues(1, n, [q], 2)
+        fa, fb = oracle.ntt(a, t)[0], oracle.ntt(b, t)[0]
+        prod = np.array([int(x) * int(y) % q for x, y in zip(fa, fb)], dtype=np.uint64)
+        c = oracle.ntt(prod[None], t, inverse=True)[0]
+        assert c.tolist() == cf.negacyclic(a[0].tolist(), b[0].tolist(), q)
+
+
+def test_modmul_primitives():
+    rng = random.Random(5)
+    for q in cf.LOCKED_PRIMES + cf.primes_below(50, 16384, 2) + [(1 << 62) - 57]:
+        vals = [0, 1, q - 1, q // 2] + [rng.randrange(q) for _ in range(200)]
+        for a in vals[:40]:
+            for b in vals[::13]:
+                assert oracle.lib().orc_mul_barrett(a, b, q) == a * b % q
+                wq = (b << 64) // q
+                assert oracle.lib().orc_mul_shoup(a, b, wq, q) == a * b % q
+
+
+def test_galois_and_monomial_shift():
+    log_n = 5
+    n = 1 << log_n
+    q = cf.LOCKED_PRIMES[3]
+    a = oracle.fill_residues(1, n, [q], 3)[0]
+    for g in (1, 3, 5, 17, 2 * n - 1):
+        assert oracle.galois(a, q, log_n, g).tolist() == cf.galois(a.tolist(), g, q)
+    for e in (0, 1, 7, n, n + 3, 2 * n - 1):
+        mono = [0] * n
+        if e % (2 * n) < n:
+            mono[e % (2 * n)] = 1
+        else:
+            mono[e % (2 * n) - n] = q - 1
+        assert oracle.monomial_shift(a, q, log_n, e).tolist() == cf.negacyclic(a.tolist(), mono, q)
+
+
+def test_keyswitch_fixture(golden_dir):
+    data = np.load(os.path.join(golden_dir, "keyswitch_small.npz"))
+    tags = sorted({k.rsplit("_", 1)[0] for k in data.files})
+    assert len(tags) == 20
+    for tag in tags:
+        q = data[tag + "_q"]
+        dnum, g, n = (int(v) for v in data[tag + "_meta"])
+        got = oracle.keyswitch(data[tag + "_ct"][None], data[tag + "_key"], q, dnum, n.bit_length() - 1, g)
+        np.testing.assert_array_equal(got[0], data[tag + "_out"], err_msg=tag)
+
+
+def _ternary(rng, n):
+    return [rng.choice((-1, 0, 1)) for _ in range(n)]
+
+
+def _bfv_keyswitch_roundtrip(q, dnum, g, log_n, seed):
+    """Encrypt under s_old, keyswitch with a key built for (sigma_g(s_old) -> s_new),
+    decrypt under s_new: must give sigma_g(m)."""
+    rng = random.Random(seed)
+    n = 1 << log_n
+    L = len(q) - 1
+    p = q[L]
+    t = 1 << 59
+    Q = 1
+    for x in q[:L]:
+        Q *= x
+    s_old, s_new = _ternary(rng, n), _ternary(rng, n)
+    psis = [cf.minimal_psi(x, n) for x in q]
+    s_rot = cf.galois([v % (1 << 200) for v in s_old], g, 1 << 200)  # exact: sign handled below
+    s_rot = [v - (1 << 200) if v > (1 << 199) else v for v in s_rot]
+    key = []
+    for j in range(dnum):
+        digit = cf.digit_primes(L, dnum, j)
+        comp = [[], []]
+        e = [rng.randrange(-3, 4) for _ in range(n)]  # one integer error polynomial for all primes
+        for ti, qt in enumerate(q):
+            a = [rng.randrange(qt) for _ in range(n)]
+            b = [(x + y) % qt for x, y in zip(cf.negacyclic([-v for v in a], s_new, qt), e)]
+            if ti in digit:
+                b = [(x + (p % qt) * v) % qt for x, v in zip(b, s_rot)]
+            comp[0].append(cf.ntt(b, qt, psis[ti]))
+            comp[1].append(cf.ntt(a, qt, psis[ti]))
+        key.append(comp)
+    m = [rng.randrange(t) for _ in range(n)]
+    a = [rng.randrange(Q) for _ in range(n)]
+    e = [rng.randrange(-3, 4) for _ in range(n)]
+    delta = Q // t
+    c0 = [(x + y + delta * z) % Q for x, y, z in zip(cf.negacyclic([-v for v in a], s_old, Q), e, m)]
+    ct = np.array([[[v % qi for v in c0] for qi in q[:L]], [[v % qi for v in a] for qi in q[:L]]], dtype=np.uint64)
+    out = oracle.keyswitch(ct[None], np.array(key, dtype=np.uint64), q, dnum, log_n, g)[0]
+    d0 = [cf.crt([int(out[0][i][k]) for i in range(L)], q[:L]) for k in range(n)]
+    d1 = [cf.crt([int(out[1][i][k]) for i in range(L)], q[:L]) for k in range(n)]
+    phase = [(x + y) % Q for x, y in zip(d0, cf.negacyclic(d1, s_new, Q))]
+    dec = [((t * v + Q // 2) // Q) % t for v in phase]
+    assert dec == cf.galois(m, g, t)
+
+
+@pytest.mark.parametrize("dnum,g", [(6, 1), (6, 3), (3, 1), (3, 2 * 32 - 1), (2, 5)])
+def test_keyswitch_decrypts(dnum, g):
+    log_n = 5
+    n = 1 << log_n
+    if dnum == 6:
+        q = cf.LOCKED_PRIMES
+    else:
+        q = cf.primes_below(50, n, 6) + cf.primes_below(60, n, 1)
+    _bfv_keyswitch_roundtrip(q, dnum, g, log_n, seed=dnum * 100 + g)
+
+
+def test_share_gemm_fixture(golden_dir):
+    data = np.load(os.path.join(golden_dir, "gemm_small.npz"))
+    for name in ("i8_a", "i8_shift59", "i32_a", "i32_shift59"):
+        sh = data[name + "_shift"] if name + "_shift" in data.files else None
+        got = oracle.share_gemm(data[name + "_x"], data[name + "_w"], sh, int(data[name + "_mask"][0]))
+        np.testing.assert_array_equal(got, data[name + "_y"], err_msg=name)
+    yc = oracle.share_gemm(data["probe_client"], data["probe_weight"], None, 59)
+    ys = oracle.share_gemm(data["probe_server"], data["probe_weight"], None, 59)
+    recon = (yc + ys) & np.uint64((1 << 59) - 1)
+    np.testing.assert_array_equal(recon, data["probe_plain"])
+
+
+def test_share_gemm_numpy_wraps():
+    x = oracle.fill_u64(7 * 300, 11).reshape(7, 300)
+    w = oracle.fill_i8(5 * 300, 12).reshape(5, 300)
+    want = x @ w.astype(np.int64).astype(np.uint64).T  # numpy integer matmul wraps mod 2^64
+    np.testing.assert_array_equal(oracle.share_gemm(x, w), want)
+
+
+def test_lift_and_local_scale():
+    t = 1 << 59
+    for q in cf.LOCKED_PRIMES[:6]:
+        for v in (0, 1, (1 << 58) - 1, 1 << 58, t - 1, t - 5):
+            signed = v - t if v >= (1 << 58) else v
+            assert oracle.lift59(v, q) == signed % q
+    q = cf.LOCKED_PRIMES[:6]
+    Q = 1
+    for x in q:
+        Q *= x
+    delta = [(Q // t) % x for x in q]
+    r = Q % t
+    shares = oracle.fill_u64(2 * 50, 3).reshape(2, 50) & np.uint64(t - 1)
+    w = oracle.fill_u64(50, 4) & np.uint64(t - 1)
+    got = oracle.local_dot_scale(shares, w, delta, r, q)
+    for s in range(2):
+        m = sum(int(a) * int(b) for a, b in zip(shares[s], w)) % t
+        want = [((Q * m + t // 2) // t) % x for x in q]  # round(Q*m/t) mod q_k
+        assert got[s].tolist() == want
