@@ -1,0 +1,270 @@
+"""Benchmark of the BFV hot path on one MI355X.
+
+Primary line (the workload BASELINE's metric is quoted on): batched forward +
+inverse negacyclic NTT at N=16384 over six ~50-bit primes, 256 ciphertexts x 2
+polynomials = 3072 limbs (one step = one forward and one inverse launch over
+all limbs).  Also reported in the same JSON line: the C3 keyswitch (dnum=3,
+64 ciphertexts, 64 independent keys) and the C4 share GEMM (512x1024x3072,
+int8 weights, mod 2^64).  Inputs are generated on the GPU and are resident in
+HBM before timing; every timed result is checked afterwards (round trip,
+re-run equality) and a slice is compared with the oracle.
+
+The cpu_baseline legs time the C oracle (oracle/, the same algorithms in
+scalar C, OpenMP over limbs/ciphertexts/rows) on bounded samples of the same
+workloads.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "privacy-rag_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "keyswitch/s and NTT/s at N=16384 L=6; share-GEMM TOPS; % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+I8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+N = 16384
+LOG_N = 14
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on (torch's current stream)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, steps: int, warmup: int) -> float:
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps  # ms per step
+
+
+def bench_ntt(torch, praghip, steps, warmup):
+    from praghip import params, synth
+    q = params.c2_primes()
+    limbs = 256 * 2 * 6
+    data = torch.empty(limbs * N, dtype=torch.int64, device="cuda")
+    synth.fill_residues(data, q, LOG_N, 0x5052414700000002)
+    ref = data.clone()
+    plan = praghip.NttBatch(q, LOG_N)
+
+    def step():
+        plan.forward(data)
+        plan.inverse(data)
+
+    ms = Timer(torch).run(step, steps, warmup)
+    assert torch.equal(data, ref), "NTT round trip changed the data"
+    launch_ms = ms / 2
+    bytes_per_launch = limbs * 2 * N * 8
+    gbs = bytes_per_launch / (launch_ms * 1e-3) / 1e9
+    return {
+        "limbs": limbs, "q": q, "ms_per_step": ms, "launch_ms": launch_ms,
+        "ntt_per_s": 2 * limbs / (ms * 1e-3), "poly_ntt_per_s": 2 * limbs / 6 / (ms * 1e-3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "ntt_kernel<14> (forward and inverse launches)",
+                     "algorithmic_bytes_per_launch": bytes_per_launch},
+    }
+
+
+def bench_keyswitch(torch, praghip, steps, warmup):
+    from praghip import params, synth
+    q = params.c3_primes()
+    L, dnum, batch = 6, 3, 64
+    sw = praghip.Switch(q, LOG_N, dnum, max_batch=batch)
+    ct = torch.empty(batch * 2 * L * N, dtype=torch.int64, device="cuda")
+    out = torch.empty_like(ct)
+    keys = torch.empty(batch * sw.key_words, dtype=torch.int64, device="cuda")
+    synth.fill_residues(ct, q[:L], LOG_N, 0x5052414700000003)
+    synth.fill_residues(keys, q, LOG_N, 0x5052414700000103)
+
+    def step():
+        sw.keyswitch(ct, out, keys=keys, key_stride=sw.key_words, galois=1)
+
+    ms = Timer(torch).run(step, steps, warmup)
+    first = out.clone()
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(first, out), "keyswitch not deterministic"
+    bytes_per_ks = 8 * N * (2 * L + 2 * L + dnum * 2 * (L + 1))
+    gbs = batch * bytes_per_ks / (ms * 1e-3) / 1e9
+    return {
+        "batch": batch, "dnum": dnum, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole keyswitch (ModUp, NTT, product, INTT, ModDown)",
+                     "algorithmic_bytes_per_keyswitch": bytes_per_ks},
+        "_tensors": (ct, keys, out, q),
+    }
+
+
+def bench_gemm(torch, praghip, steps, warmup):
+    from praghip import synth
+    m, k, n = 512, 1024, 3072
+    x = torch.empty(m * k, dtype=torch.int64, device="cuda").view(m, k)
+    w = torch.empty(n * k, dtype=torch.int8, device="cuda").view(n, k)
+    y = torch.empty((m, n), dtype=torch.int64, device="cuda")
+    synth.fill_u64(x, 0x5052414700000004)
+    synth.fill_i8(w, 0x5052414700000104)
+
+    def step():
+        praghip.share_gemm(x, w, y=y)
+
+    ms = Timer(torch).run(step, steps, warmup)
+    tops = 2 * m * k * n / (ms * 1e-3) / 1e12
+    mfma_tops = 8 * tops  # eight i8 digit products per u64 x i8 product
+    return {
+        "shape": [m, k, n], "ms_per_step": ms, "tops": tops,
+        "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "share_gemm_kernel<8> (i8 MFMA ops executed)"},
+        "_tensors": (x, w, y),
+    }
+
+
+def cpu_baselines(torch, res, budget_s: float):
+    """Oracle timings on bounded samples (rank 0, N=1 only)."""
+    import numpy as np
+
+    import oracle
+    threads = len(os.sched_getaffinity(0))
+    out = {}
+    # NTT: sample of the C2 batch, all host threads
+    q = res["ntt"]["q"]
+    tab = oracle.Tables(q, LOG_N)
+    limbs = 384
+    a = oracle.fill_residues(limbs, N, q, 0x5052414700000002)
+    t0 = time.perf_counter()
+    fa = oracle.ntt(a, tab, threads=threads)
+    oracle.ntt(fa, tab, inverse=True, threads=threads)
+    dt = time.perf_counter() - t0
+    reps = max(1, int(budget_s / 3 / max(dt, 1e-3)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.ntt(oracle.ntt(a, tab, threads=threads), tab, inverse=True, threads=threads)
+    dt = (time.perf_counter() - t0) / reps
+    out["ntt"] = {"value": 2 * limbs / dt, "unit": "limb-NTT/s", "cores": threads, "kind": "port",
+                  "sample": f"{limbs} limbs of the C2 batch, forward+inverse, x{reps}"}
+    # keyswitch: 4 ciphertexts of C3 with their keys
+    ct_t, keys_t, out_t, q3 = res["keyswitch"]["_tensors"]
+    nb = 2 * threads if threads <= 8 else threads
+    nb = min(nb, 64)
+    ct = ct_t[: nb * 2 * 6 * N].cpu().numpy().view(np.uint64).reshape(nb, 2, 6, N)
+    kw = 3 * 2 * 7 * N
+    keys = keys_t[: nb * kw].cpu().numpy().view(np.uint64).reshape(nb, 3, 2, 7, N)
+    tab3 = oracle.Tables(q3, LOG_N)
+    t0 = time.perf_counter()
+    got = oracle.keyswitch(ct, keys, q3, 3, LOG_N, 1, tables=tab3, per_ct_keys=True, threads=threads)
+    dt = time.perf_counter() - t0
+    gpu_slice = out_t[: nb * 2 * 6 * N].cpu().numpy().view(np.uint64).reshape(nb, 2, 6, N)
+    out["keyswitch_parity"] = bool(np.array_equal(got, gpu_slice))
+    out["keyswitch"] = {"value": nb / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
+                        "sample": f"{nb} C3 ciphertexts (dnum=3) with their own keys"}
+    # GEMM: 64 rows of the C4 activations against all 3072 weight rows
+    x_t, w_t, y_t = res["gemm"]["_tensors"]
+    rows = 64
+    x = x_t[:rows].cpu().numpy().view(np.uint64)
+    w = w_t.cpu().numpy()
+    t0 = time.perf_counter()
+    y = oracle.share_gemm(x, w, threads=threads)
+    dt = time.perf_counter() - t0
+    out["gemm_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
+    out["gemm"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+                   "sample": f"{rows} of 512 activation rows x 1024 x 3072"}
+    # NTT parity on a slice of the timed batch
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    import praghip
+    assert torch.cuda.is_available() and praghip.device_count() >= 1, "needs an MI355X"
+    res = {}
+    if args.only in ("all", "ntt"):
+        log("NTT C2 ...")
+        res["ntt"] = bench_ntt(torch, praghip, args.steps, args.warmup)
+        log(f"NTT {res['ntt']['ntt_per_s']:.4g} limb-NTT/s, {res['ntt']['roofline']['achieved']} GB/s")
+    if args.only in ("all", "keyswitch"):
+        log("keyswitch C3 ...")
+        res["keyswitch"] = bench_keyswitch(torch, praghip, args.steps, args.warmup)
+        log(f"keyswitch {res['keyswitch']['keyswitch_per_s']:.4g}/s")
+    if args.only in ("all", "gemm"):
+        log("share GEMM C4 ...")
+        res["gemm"] = bench_gemm(torch, praghip, args.steps, args.warmup)
+        log(f"GEMM {res['gemm']['tops']:.4g} TOPS")
+    cpu = {}
+    if not args.no_cpu and args.only == "all":
+        log("oracle CPU baselines ...")
+        cpu = cpu_baselines(torch, res, args.cpu_budget)
+        log(f"cpu: {json.dumps(cpu)}")
+
+    def clean(d):
+        return {k: v for k, v in d.items() if not k.startswith("_")}
+
+    primary = res.get("ntt") or res.get("keyswitch") or res.get("gemm")
+    key = "ntt" if "ntt" in res else ("keyswitch" if "keyswitch" in res else "gemm")
+    value = {"ntt": lambda r: r["ntt_per_s"], "keyswitch": lambda r: r["keyswitch_per_s"],
+             "gemm": lambda r: r["tops"]}[key](primary)
+    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "gemm": "TOPS"}[key]
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": primary["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64" if key == "ntt" else ("u64+f64" if key == "keyswitch" else "i8"),
+        "data": "synthetic (seeded splitmix64 on the GPU)",
+        "config": {"workload": {
+            "ntt": "C2: batched forward+inverse negacyclic NTT, N=16384, 6 primes ~50 bit, "
+                   "256 ciphertexts x 2 polynomials = 3072 limbs",
+            "keyswitch": "C3: keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
+            "gemm": "C4: share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64"}[key],
+            "N": N, "parallelism": "single GPU"},
+        "roofline": primary["roofline"],
+        "cpu_baseline": cpu.get(key),
+        "extra": {k: clean(v) for k, v in res.items() if k != key},
+    }
+    if cpu:
+        line["extra"]["cpu_baselines"] = {k: v for k, v in cpu.items() if k != key}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,153 @@
+/*
+ * praghip - MI355X (gfx950) backend for the BFV polynomial engine and the
+ * party-local Z_2^64 share GEMM of HaoR265/privacy-rag.
+ *
+ * C ABI: plain pointers and sizes, integer status codes, a thread-local error
+ * string, no exceptions across the boundary and no silent CPU fallback.  Each
+ * entry point names the reference interface it replaces (paths relative to
+ * implementation_v1/).
+ *
+ * Layouts are the reference's: coefficient-major little-endian u64,
+ * [batch][component][prime][N] for ciphertexts (ntt.hpp:20, switch.cu:65,71),
+ * [digit][component][key prime][N] NTT-form keys (keyswitch/seal_adapter.cpp:37-39),
+ * [prime][N][2] (operand, quotient) NTT tables (seal_tables.cpp:22-33) and
+ * [out][in] weights (bfv_matrix.inc:101-105, artifacts.hpp:86-92).
+ *
+ * Pointers documented "device" are HIP device pointers on the plan's device;
+ * "host" pointers are ordinary host memory.  `stream` is a hipStream_t used as
+ * given (NULL is the HIP null stream).  Device-pointer entry points are
+ * asynchronous on that stream; host-pointer entry points run on the plan's own
+ * stream and are synchronous.
+ *
+ * After a HIP runtime error a plan releases itself (wipes and frees its
+ * buffers) and every later call returns PRAGHIP_E_CLOSED, as the reference's
+ * backends do (switch.cu:124, ntt.cu:163-167).
+ */
+#ifndef PRAGHIP_H
+#define PRAGHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; praghip_last_error() returns the reference's public code text
+ * (E_NTT_SHAPE, E_NTT_CANONICAL_REQUIRED, E_SWITCH_CLOSED, ...). */
+#define PRAGHIP_OK 0
+#define PRAGHIP_E_SHAPE 1     /* E_NTT_SHAPE / E_SWITCH_SHAPE (ntt.cu:106, switch.cu:114) */
+#define PRAGHIP_E_CANONICAL 2 /* E_NTT_CANONICAL_REQUIRED (ntt.cu:107) */
+#define PRAGHIP_E_CONTEXT 3   /* E_NTT_CONTEXT: primes/tables rejected (seal_tables.cpp:11) */
+#define PRAGHIP_E_CLOSED 4    /* E_NTT_CLOSED / E_SWITCH_CLOSED (ntt.cu:146, switch.cu:114) */
+#define PRAGHIP_E_DEVICE 5    /* E_NTT_CUDA equivalent: HIP runtime error (ntt.cu:11) */
+#define PRAGHIP_E_ARGUMENT 6  /* null pointer, bad Galois element, bad dtype */
+#define PRAGHIP_E_STATE 7     /* E_CLIENT_KEY_STATE (ntt.cu:175,182) */
+
+/* Cleanup report of close(): Cleanup{first_cuda_error, wipe_synchronized_bytes,
+ * freed_bytes, closed} (ntt.hpp:15-19, switch.hpp:11). */
+typedef struct praghip_cleanup {
+  int32_t first_hip_error;
+  int32_t closed;
+  uint64_t wipe_synchronized_bytes;
+  uint64_t freed_bytes;
+} praghip_cleanup;
+
+/* Timing of the last host-buffer call (ntt.hpp:10-14, switch.hpp:10). */
+typedef struct praghip_timing {
+  double upload_ms, kernel_ms, download_ms;
+  uint64_t device_bytes, sensitive_bytes;
+} praghip_timing;
+
+const char *praghip_last_error(void);
+int praghip_version(void);
+/* Number of visible gfx950 devices (0 without a GPU; never initialises HIP
+ * when the runtime reports no device). */
+int praghip_device_count(void);
+
+/* ---------------------------------------------------------------- tables */
+/* SEAL NTTTables for one prime q == 1 mod 2N, q < 2^62 (the arrays
+ * seal_tables.cpp:22-33 extracts): fwd_pairs/inv_pairs [N][2], invn_pair [2].
+ * Also returns the minimal primitive 2N-th root if psi != NULL. */
+int praghip_ntt_tables(uint64_t q, uint32_t log_n, uint64_t *fwd_pairs, uint64_t *inv_pairs,
+                       uint64_t *invn_pair, uint64_t *psi);
+
+/* ------------------------------------------------------------- NttBatch */
+/* prag::experimental::ntt::NttBatch (ntt.hpp:22-40).  Tables may be NULL
+ * (generated from q); when given they are validated against q.  `batches`
+ * sizes the plan's own buffer for the host-vector calls; 4 <= log_n <= 14. */
+typedef struct praghip_ntt_plan praghip_ntt_plan;
+int praghip_ntt_plan_create(int device, const uint64_t *q, size_t primes, uint32_t log_n,
+                            const uint64_t *fwd_pairs, const uint64_t *inv_pairs,
+                            const uint64_t *invn_pairs, size_t batches, praghip_ntt_plan **plan);
+/* In-place batched transforms over device [limbs][N], limb l on prime l % primes
+ * (ntt.cu:104-127 stage loop).  forward: natural -> bit-reversed order;
+ * inverse: bit-reversed -> natural.  Inputs must be canonical. */
+int praghip_ntt_forward(praghip_ntt_plan *plan, uint64_t *data, size_t limbs, void *stream);
+int praghip_ntt_inverse(praghip_ntt_plan *plan, uint64_t *data, size_t limbs, void *stream);
+/* NttBatch::transform (ntt.cu:145-168): host [batches][primes][N] in and out,
+ * canonical-input check, synchronous. */
+int praghip_ntt_transform(praghip_ntt_plan *plan, const uint64_t *input, uint64_t *output, int inverse);
+/* NttBatch::bind_client_key (ntt.hpp:28, seal_tables.cpp:39-53): host [primes][N]
+ * NTT-form secret key, canonical. */
+int praghip_ntt_bind_client_key(praghip_ntt_plan *plan, const uint64_t *key);
+/* NttBatch::client_phase (ntt.cu:181-199): NTT -> (.) key -> INTT, host buffers. */
+int praghip_ntt_client_phase(praghip_ntt_plan *plan, const uint64_t *input, uint64_t *output);
+int praghip_ntt_sync(praghip_ntt_plan *plan);
+int praghip_ntt_timing(const praghip_ntt_plan *plan, praghip_timing *out);
+/* NttBatch::close (ntt.cu:103-121): idempotent wipe + free. */
+int praghip_ntt_close(praghip_ntt_plan *plan, praghip_cleanup *out);
+void praghip_ntt_destroy(praghip_ntt_plan *plan);
+
+/* --------------------------------------------------------------- Switch */
+/* prag::experimental_full_switch::Switch (switch.hpp:12-28), generalised to
+ * dnum digits: q has L+1 primes, q[L] is the special prime; key is the host
+ * [dnum][2][L+1][N] NTT-form switching key for `element` (NULL: keys are passed
+ * per call).  dnum = L reproduces the reference exactly (one prime per digit,
+ * no base conversion); dnum < L uses fast base conversion (ModUp).  max_batch
+ * sizes the plan's scratch.  L+1 <= 16. */
+typedef struct praghip_switch_plan praghip_switch_plan;
+int praghip_switch_plan_create(int device, const uint64_t *q, size_t data_primes, uint32_t log_n,
+                               size_t dnum, const uint64_t *key, uint32_t element, size_t max_batch,
+                               praghip_switch_plan **plan);
+/* Switch::apply (keyswitch/seal_adapter.cpp:44-52 + switch.cu:113-125): host
+ * [2][L][N] coefficient-form ciphertext -> Galois(element) + keyswitch -> host
+ * [2][L][N]. */
+int praghip_switch_apply(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output);
+/* Batched device keyswitch: in/out device [batch][2][L][N]; keys device
+ * [dnum][2][L+1][N] per ciphertext at key_stride words apart (0: one shared
+ * key; NULL keys: the plan's key).  galois_elt odd, < 2N (1 = plain switch). */
+int praghip_keyswitch(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output, size_t batch,
+                      const uint64_t *keys, size_t key_stride, uint32_t galois_elt, void *stream);
+int praghip_switch_sync(praghip_switch_plan *plan);
+int praghip_switch_timing(const praghip_switch_plan *plan, praghip_timing *out);
+int praghip_switch_close(praghip_switch_plan *plan, praghip_cleanup *out);
+void praghip_switch_destroy(praghip_switch_plan *plan);
+
+/* ------------------------------------------------------ share GEMM (ring) */
+/* Party-local share GEMM, the loop of bfv_matrix.inc:101-105/156-160/177-182
+ * (and batch_matrix.inc:120-156) as a LocalShares operation
+ * (local_shares.hpp:22-32): y[m][n] = ((sum_k x[m][k] * w[n][k]) << shifts[n])
+ * mod 2^mask_bits, x u64 device [M][K], w signed device [N][K] (w_bits 8: int8;
+ * 32: int32 in [-0x808080, 0x7F7F7F], three balanced signed bytes; the
+ * reference f12 domain is |w| <= 2^20),
+ * shifts device int8 [N] in [0,63] or NULL, y u64 device [M][N]; mask_bits 59
+ * is the reference ring, 64 is no mask.  Asynchronous on `stream` (NULL: the
+ * null stream of `device`). */
+int praghip_share_gemm(int device, const uint64_t *x, const void *w, int w_bits, const int8_t *shifts,
+                       uint64_t *y, size_t m, size_t k, size_t n, int mask_bits, void *stream);
+
+/* ------------------------------------------------------ synthetic inputs */
+/* Seeded counter-based inputs (no counterpart in the reference, whose probes
+ * draw from mt19937_64, check_resident.cpp:26): element i of the buffer is
+ * splitmix64(seed + (i+1)*0x9E3779B97F4A7C15).  Residues: mulhi(z, q[limb % primes])
+ * over device [limbs][2^log_n]; u64: z; int8: mulhi(z, 255) - 127. */
+int praghip_fill_residues(int device, uint64_t *data, size_t limbs, uint32_t log_n, const uint64_t *q,
+                          size_t primes, uint64_t seed, void *stream);
+int praghip_fill_u64(int device, uint64_t *data, size_t count, uint64_t seed, void *stream);
+int praghip_fill_i8(int device, int8_t *data, size_t count, uint64_t seed, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PRAGHIP_H */

@@ -1,0 +1,790 @@
+// C ABI of praghip (include/praghip.h): plans, validation, error codes,
+// wipe-on-close, and the launches of the gfx950 kernels.
+//
+// Plans mirror the reference's backend objects (NttBatch ntt.cu:99-171,
+// Switch switch.cu:84-217): they own their device buffers and one stream,
+// validate shapes and canonical inputs before touching the device, release
+// themselves after any HIP error, and report Cleanup{first error, wiped bytes,
+// freed bytes, closed} from an idempotent close().
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/praghip.h"
+#include "kernels.hpp"
+
+namespace praghip {
+hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
+                             int M, int K, int N, int mask_bits, hipStream_t s);
+}
+
+using namespace praghip;
+using u128 = unsigned __int128;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& text) {
+  g_error = text;
+  return code;
+}
+
+// ------------------------------------------------------------ number theory
+uint64_t mulmod(uint64_t a, uint64_t b, uint64_t q) { return uint64_t((u128)a * b % q); }
+uint64_t powmod(uint64_t a, uint64_t e, uint64_t q) {
+  uint64_t r = 1 % q;
+  a %= q;
+  for (; e; e >>= 1) {
+    if (e & 1) r = mulmod(r, a, q);
+    a = mulmod(a, a, q);
+  }
+  return r;
+}
+uint64_t invmod(uint64_t a, uint64_t q) { return powmod(a % q, q - 2, q); }  // q prime
+bool is_prime(uint64_t n) {
+  static const uint64_t bases[] = {2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37};
+  if (n < 2) return false;
+  for (uint64_t b : bases) {
+    if (n == b) return true;
+    if (n % b == 0) return false;
+  }
+  uint64_t d = n - 1;
+  int s = 0;
+  while (!(d & 1)) {
+    d >>= 1;
+    ++s;
+  }
+  for (uint64_t b : bases) {
+    uint64_t x = powmod(b, d, n);
+    if (x == 1 || x == n - 1) continue;
+    bool comp = true;
+    for (int r = 1; r < s && comp; ++r) {
+      x = mulmod(x, x, n);
+      if (x == n - 1) comp = false;
+    }
+    if (comp) return false;
+  }
+  return true;
+}
+uint64_t shoup_q(uint64_t w, uint64_t q) { return uint64_t(((u128)w << 64) / q); }
+uint64_t bitrev(uint64_t x, unsigned bits) {
+  uint64_t r = 0;
+  for (unsigned i = 0; i < bits; ++i) r |= ((x >> i) & 1) << (bits - 1 - i);
+  return r;
+}
+// Smallest primitive 2N-th root of unity (SEAL try_minimal_primitive_root).
+uint64_t minimal_root(uint64_t q, uint64_t two_n) {
+  if ((q - 1) % two_n) return 0;
+  uint64_t g = 0;
+  for (uint64_t x = 2; x < q && !g; ++x) {
+    const uint64_t c = powmod(x, (q - 1) / two_n, q);
+    if (powmod(c, two_n / 2, q) == q - 1) g = c;
+  }
+  if (!g) return 0;
+  const uint64_t g2 = mulmod(g, g, q);
+  uint64_t cur = g, best = g;
+  for (uint64_t i = 0; i < two_n; i += 2) {
+    best = cur < best ? cur : best;
+    cur = mulmod(cur, g2, q);
+  }
+  return best;
+}
+// SEAL NTTTables (seal_tables.cpp:22-33 exports them): forward[bitrev(i)] = psi^i,
+// inverse[bitrev(i-1)+1] = psi^-i, invn = N^-1; each as (operand, quotient).
+bool make_tables(uint64_t q, unsigned log_n, uint64_t* fwd, uint64_t* inv, uint64_t* invn, uint64_t* psi_out) {
+  const uint64_t n = 1ull << log_n;
+  const uint64_t psi = minimal_root(q, 2 * n);
+  if (!psi) return false;
+  const uint64_t psi_inv = invmod(psi, q);
+  fwd[0] = 1;
+  fwd[1] = shoup_q(1, q);
+  inv[0] = 1;
+  inv[1] = shoup_q(1, q);
+  uint64_t p = psi, pi = psi_inv;
+  for (uint64_t i = 1; i < n; ++i) {
+    const uint64_t f = bitrev(i, log_n), r = bitrev(i - 1, log_n) + 1;
+    fwd[2 * f] = p;
+    fwd[2 * f + 1] = shoup_q(p, q);
+    inv[2 * r] = pi;
+    inv[2 * r + 1] = shoup_q(pi, q);
+    p = mulmod(p, psi, q);
+    pi = mulmod(pi, psi_inv, q);
+  }
+  const uint64_t ni = invmod(n % q, q);
+  invn[0] = ni;
+  invn[1] = shoup_q(ni, q);
+  if (psi_out) *psi_out = psi;
+  return true;
+}
+
+// --------------------------------------------------------------- device side
+class DeviceScope {
+ public:
+  explicit DeviceScope(int target) {
+    status_ = hipGetDevice(&previous_);
+    if (status_ == hipSuccess && previous_ != target) {
+      status_ = hipSetDevice(target);
+      restore_ = status_ == hipSuccess;
+    }
+  }
+  ~DeviceScope() {
+    if (restore_) (void)hipSetDevice(previous_);
+  }
+  hipError_t status() const { return status_; }
+
+ private:
+  int previous_ = 0;
+  bool restore_ = false;
+  hipError_t status_ = hipSuccess;
+};
+
+int check_device(int device) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return fail(PRAGHIP_E_DEVICE, "E_GFX950_REQUIRED: no HIP device");
+  if (device < 0 || device >= count) return fail(PRAGHIP_E_ARGUMENT, "E_DEVICE_INDEX");
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return fail(PRAGHIP_E_DEVICE, "E_DEVICE_PROPERTIES");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(PRAGHIP_E_DEVICE, std::string("E_GFX950_REQUIRED: ") + prop.gcnArchName);
+  return PRAGHIP_OK;
+}
+
+// Allocation registry: every device buffer of a plan, sensitive or public.
+struct Buffers {
+  struct Entry {
+    void** slot;
+    size_t bytes;
+    bool sensitive;
+  };
+  std::vector<Entry> entries;
+  hipError_t alloc(void** slot, size_t bytes, bool sensitive) {
+    *slot = nullptr;
+    if (!bytes) return hipSuccess;
+    const hipError_t e = hipMalloc(slot, bytes);
+    if (e == hipSuccess) entries.push_back({slot, bytes, sensitive});
+    return e;
+  }
+  size_t sensitive_bytes() const {
+    size_t s = 0;
+    for (auto& e : entries) s += e.sensitive ? e.bytes : 0;
+    return s;
+  }
+  size_t total_bytes() const {
+    size_t s = 0;
+    for (auto& e : entries) s += e.bytes;
+    return s;
+  }
+};
+
+// Shared release: wipe sensitive buffers, synchronise, free everything.
+void release_all(int device, Buffers& buf, hipStream_t& stream, hipEvent_t* events, int nevents, praghip_cleanup& c,
+                 bool& closing) {
+  closing = true;
+  if (c.closed) return;
+  auto ok = [&](hipError_t e) {
+    if (e != hipSuccess && !c.first_hip_error) c.first_hip_error = int(e);
+    return e == hipSuccess;
+  };
+  if (device < 0) {
+    c.closed = 1;
+    return;
+  }
+  DeviceScope scope(device);
+  if (!ok(scope.status())) return;
+  uint64_t queued = 0;
+  for (auto& e : buf.entries)
+    if (e.sensitive && *e.slot && ok(hipMemsetAsync(*e.slot, 0, e.bytes, stream))) queued += e.bytes;
+  if (ok(stream ? hipStreamSynchronize(stream) : hipDeviceSynchronize())) c.wipe_synchronized_bytes += queued;
+  bool all_freed = true;
+  for (auto& e : buf.entries) {
+    if (!*e.slot) continue;
+    if (ok(hipFree(*e.slot))) {
+      *e.slot = nullptr;
+      if (e.sensitive) c.freed_bytes += e.bytes;
+    } else {
+      all_freed = false;
+    }
+  }
+  bool events_gone = true;
+  for (int i = 0; i < nevents; ++i)
+    if (events[i]) {
+      if (ok(hipEventDestroy(events[i]))) events[i] = nullptr;
+      else events_gone = false;
+    }
+  if (stream && ok(hipStreamDestroy(stream))) stream = nullptr;
+  c.closed = all_freed && events_gone && !stream;
+}
+
+struct NttHost {
+  std::vector<NttPrime> primes;
+  std::vector<ulonglong2> fwd_u, inv_u;
+  std::vector<double2> fwd_f, inv_f;
+};
+
+// Builds the per-prime constants and device-format tables of a prime set.
+int build_ntt_host(const uint64_t* q, size_t P, unsigned log_n, const uint64_t* fwd_in, const uint64_t* inv_in,
+                   const uint64_t* invn_in, NttHost& h) {
+  const size_t n = size_t(1) << log_n;
+  h.primes.resize(P);
+  h.fwd_u.resize(P * n);
+  h.inv_u.resize(P * n);
+  h.fwd_f.resize(P * n);
+  h.inv_f.resize(P * n);
+  std::vector<uint64_t> fwd(2 * n), inv(2 * n), invn(2);
+  for (size_t p = 0; p < P; ++p) {
+    const uint64_t qq = q[p];
+    if (qq < 3 || qq >= (1ull << 62) || !is_prime(qq) || (qq - 1) % (2 * n))
+      return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT: q must be a prime < 2^62 with q == 1 mod 2N");
+    for (size_t p2 = 0; p2 < p; ++p2)
+      if (q[p2] == qq) return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT: repeated prime");
+    if (!make_tables(qq, log_n, fwd.data(), inv.data(), invn.data(), nullptr))
+      return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT: no 2N-th root");
+    if ((fwd_in && std::memcmp(fwd_in + p * 2 * n, fwd.data(), 16 * n)) ||
+        (inv_in && std::memcmp(inv_in + p * 2 * n, inv.data(), 16 * n)) ||
+        (invn_in && std::memcmp(invn_in + p * 2, invn.data(), 16)))
+      return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT: tables are not the SEAL tables of q");
+    NttPrime& pr = h.primes[p];
+    std::memset(&pr, 0, sizeof(pr));
+    pr.q = qq;
+    pr.q2 = 2 * qq;
+    pr.ninv = invn[0];
+    pr.ninv_q = invn[1];
+    const uint64_t w_last = inv[2 * (n - 1)];
+    const uint64_t last = mulmod(w_last, invn[0], qq);
+    pr.last = last;
+    pr.last_q = shoup_q(last, qq);
+    pr.use_f64 = qq < (1ull << 50);
+    pr.qd = double(qq);
+    pr.qinv = 1.0 / double(qq);
+    pr.ninv_f = double(invn[0]);
+    pr.ninv_fq = double(invn[0]) / double(qq);
+    pr.last_f = double(last);
+    pr.last_fq = double(last) / double(qq);
+    for (size_t i = 0; i < n; ++i) {
+      h.fwd_u[p * n + i] = make_ulonglong2(fwd[2 * i], fwd[2 * i + 1]);
+      h.inv_u[p * n + i] = make_ulonglong2(inv[2 * i], inv[2 * i + 1]);
+      h.fwd_f[p * n + i] = make_double2(double(fwd[2 * i]), double(fwd[2 * i]) / double(qq));
+      h.inv_f[p * n + i] = make_double2(double(inv[2 * i]), double(inv[2 * i]) / double(qq));
+    }
+  }
+  return PRAGHIP_OK;
+}
+
+hipError_t upload_ntt(const NttHost& h, unsigned log_n, Buffers& buf, NttDevice& d, hipStream_t s) {
+  const size_t P = h.primes.size(), n = size_t(1) << log_n;
+  d.log_n = int(log_n);
+  d.P = int(P);
+  hipError_t e;
+  if ((e = buf.alloc((void**)&d.primes, P * sizeof(NttPrime), false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.tw_fwd_u, P * n * 16, false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.tw_inv_u, P * n * 16, false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.tw_fwd_f, P * n * 16, false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.tw_inv_f, P * n * 16, false)) != hipSuccess) return e;
+  if ((e = hipMemcpyAsync(d.primes, h.primes.data(), P * sizeof(NttPrime), hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.tw_fwd_u, h.fwd_u.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.tw_inv_u, h.inv_u.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.tw_fwd_f, h.fwd_f.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.tw_inv_f, h.inv_f.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
+  return hipStreamSynchronize(s);
+}
+
+// Device-pointer entry points run on the caller's stream as given (NULL is the
+// HIP null stream), so they order with the caller's own copies and kernels.
+hipStream_t pick(void* stream) { return static_cast<hipStream_t>(stream); }
+
+void wipe_host(std::vector<uint64_t>& v) {
+  volatile uint64_t* p = v.data();
+  for (size_t i = 0; i < v.size(); ++i) p[i] = 0;
+}
+
+}  // namespace
+
+// ============================================================== NttBatch plan
+struct praghip_ntt_plan {
+  int device = -1;
+  unsigned log_n = 0;
+  size_t P = 0, batches = 0, words = 0;
+  std::vector<uint64_t> host_q;
+  Buffers buf;
+  NttDevice d;
+  uint64_t* data = nullptr;
+  ulonglong2* client_key = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[4] = {};
+  praghip_timing timing{};
+  praghip_cleanup cleanup{};
+  bool closing = false;
+  void release() { release_all(device, buf, stream, ev, 4, cleanup, closing); }
+  ~praghip_ntt_plan() { release(); }
+};
+
+namespace {
+int device_failure(praghip_ntt_plan* p, hipError_t e, const char* what) {
+  p->release();
+  return fail(PRAGHIP_E_DEVICE, std::string("E_NTT_HIP: ") + what + ": " + hipGetErrorString(e));
+}
+bool canonical(const uint64_t* v, size_t words, const std::vector<uint64_t>& q, unsigned log_n) {
+  const size_t n = size_t(1) << log_n, P = q.size();
+  for (size_t i = 0; i < words; ++i)
+    if (v[i] >= q[(i >> log_n) % P]) return false;
+  (void)n;
+  return true;
+}
+}  // namespace
+
+extern "C" {
+
+const char* praghip_last_error(void) { return g_error.c_str(); }
+int praghip_version(void) { return 1; }
+
+int praghip_device_count(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+  int good = 0;
+  for (int i = 0; i < count; ++i) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, i) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ++good;
+  }
+  return good;
+}
+
+int praghip_ntt_tables(uint64_t q, uint32_t log_n, uint64_t* fwd_pairs, uint64_t* inv_pairs, uint64_t* invn_pair,
+                       uint64_t* psi) {
+  if (!fwd_pairs || !inv_pairs || !invn_pair) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (log_n < 1 || log_n > 17) return fail(PRAGHIP_E_SHAPE, "E_NTT_SHAPE");
+  if (q < 3 || q >= (1ull << 62) || !is_prime(q)) return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT");
+  if (!make_tables(q, log_n, fwd_pairs, inv_pairs, invn_pair, psi)) return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT");
+  return PRAGHIP_OK;
+}
+
+int praghip_ntt_plan_create(int device, const uint64_t* q, size_t primes, uint32_t log_n, const uint64_t* fwd_pairs,
+                            const uint64_t* inv_pairs, const uint64_t* invn_pairs, size_t batches,
+                            praghip_ntt_plan** plan) {
+  if (!plan || !q) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *plan = nullptr;
+  if (log_n < 4 || log_n > 14 || primes < 1 || primes > 64) return fail(PRAGHIP_E_SHAPE, "E_NTT_SHAPE");
+  NttHost h;
+  if (int rc = build_ntt_host(q, primes, log_n, fwd_pairs, inv_pairs, invn_pairs, h)) return rc;
+  if (int rc = check_device(device)) return rc;
+  std::unique_ptr<praghip_ntt_plan> p(new praghip_ntt_plan);
+  p->device = device;
+  p->log_n = log_n;
+  p->P = primes;
+  p->batches = batches;
+  p->words = batches * primes << log_n;
+  p->host_q.assign(q, q + primes);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+  for (auto& ev : p->ev)
+    if (e == hipSuccess) e = hipEventCreate(&ev);
+  if (e == hipSuccess) e = upload_ntt(h, log_n, p->buf, p->d, p->stream);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->data, p->words * 8, true);
+  if (e != hipSuccess) return device_failure(p.get(), e, "create");
+  p->timing.device_bytes = p->buf.total_bytes();
+  p->timing.sensitive_bytes = p->buf.sensitive_bytes();
+  *plan = p.release();
+  return PRAGHIP_OK;
+}
+
+static int ntt_device(praghip_ntt_plan* p, uint64_t* data, size_t limbs, void* stream, bool inverse) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_NTT_CLOSED");
+  if (!data && limbs) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (limbs > (1ull << 31)) return fail(PRAGHIP_E_SHAPE, "E_NTT_SHAPE");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_ntt(inverse, data, limbs, p->d, pick(stream));
+  if (e != hipSuccess) return device_failure(p, e, inverse ? "inverse" : "forward");
+  return PRAGHIP_OK;
+}
+
+int praghip_ntt_forward(praghip_ntt_plan* plan, uint64_t* data, size_t limbs, void* stream) {
+  return ntt_device(plan, data, limbs, stream, false);
+}
+int praghip_ntt_inverse(praghip_ntt_plan* plan, uint64_t* data, size_t limbs, void* stream) {
+  return ntt_device(plan, data, limbs, stream, true);
+}
+
+static int ntt_host_run(praghip_ntt_plan* p, const uint64_t* input, uint64_t* output, int mode) {
+  // mode 0 forward, 1 inverse, 2 client phase
+  if (!p || !input || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_NTT_CLOSED");
+  if (mode == 2 && !p->client_key) return fail(PRAGHIP_E_STATE, "E_CLIENT_KEY_STATE");
+  if (!p->words) return fail(PRAGHIP_E_SHAPE, "E_NTT_SHAPE");
+  if (!canonical(input, p->words, p->host_q, p->log_n)) return fail(PRAGHIP_E_CANONICAL, "E_NTT_CANONICAL_REQUIRED");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  const size_t bytes = p->words * 8, limbs = p->words >> p->log_n;
+  hipStream_t s = p->stream;
+  if (e == hipSuccess) e = hipEventRecord(p->ev[0], s);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->data, input, bytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[1], s);
+  if (e == hipSuccess) e = launch_ntt(mode == 1, p->data, limbs, p->d, s);
+  if (mode == 2) {
+    if (e == hipSuccess) e = launch_dyadic_shoup(p->data, p->client_key, p->d, p->words, s);
+    if (e == hipSuccess) e = launch_ntt(true, p->data, limbs, p->d, s);
+  }
+  if (e == hipSuccess) e = hipEventRecord(p->ev[2], s);
+  if (e == hipSuccess) e = hipMemcpyAsync(output, p->data, bytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[3], s);
+  if (e == hipSuccess) e = hipEventSynchronize(p->ev[3]);
+  float t01 = 0, t12 = 0, t23 = 0;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t01, p->ev[0], p->ev[1]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&t12, p->ev[1], p->ev[2]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&t23, p->ev[2], p->ev[3]);
+  if (e != hipSuccess) {
+    std::memset(output, 0, bytes);
+    return device_failure(p, e, "transform");
+  }
+  p->timing.upload_ms = t01;
+  p->timing.kernel_ms = t12;
+  p->timing.download_ms = t23;
+  return PRAGHIP_OK;
+}
+
+int praghip_ntt_transform(praghip_ntt_plan* plan, const uint64_t* input, uint64_t* output, int inverse) {
+  return ntt_host_run(plan, input, output, inverse ? 1 : 0);
+}
+
+int praghip_ntt_bind_client_key(praghip_ntt_plan* p, const uint64_t* key) {
+  if (!p || !key) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing || p->client_key) return fail(PRAGHIP_E_STATE, "E_CLIENT_KEY_STATE");
+  const size_t n = size_t(1) << p->log_n;
+  std::vector<uint64_t> pairs(2 * p->P * n);
+  for (size_t k = 0; k < p->P; ++k)
+    for (size_t i = 0; i < n; ++i) {
+      const uint64_t v = key[k * n + i];
+      if (v >= p->host_q[k]) {
+        wipe_host(pairs);
+        return fail(PRAGHIP_E_CANONICAL, "E_CLIENT_KEY_CANONICAL");
+      }
+      pairs[2 * (k * n + i)] = v;
+      pairs[2 * (k * n + i) + 1] = shoup_q(v, p->host_q[k]);
+    }
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->client_key, pairs.size() * 8, true);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->client_key, pairs.data(), pairs.size() * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  wipe_host(pairs);
+  if (e != hipSuccess) return device_failure(p, e, "bind_client_key");
+  p->timing.device_bytes = p->buf.total_bytes();
+  p->timing.sensitive_bytes = p->buf.sensitive_bytes();
+  return PRAGHIP_OK;
+}
+
+int praghip_ntt_client_phase(praghip_ntt_plan* plan, const uint64_t* input, uint64_t* output) {
+  return ntt_host_run(plan, input, output, 2);
+}
+
+int praghip_ntt_sync(praghip_ntt_plan* p) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_NTT_CLOSED");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return device_failure(p, e, "sync");
+  return PRAGHIP_OK;
+}
+
+int praghip_ntt_timing(const praghip_ntt_plan* p, praghip_timing* out) {
+  if (!p || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *out = p->timing;
+  return PRAGHIP_OK;
+}
+
+int praghip_ntt_close(praghip_ntt_plan* p, praghip_cleanup* out) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  p->release();
+  if (out) *out = p->cleanup;
+  return PRAGHIP_OK;
+}
+
+void praghip_ntt_destroy(praghip_ntt_plan* p) { delete p; }
+
+}  // extern "C"
+
+// ================================================================ Switch plan
+struct praghip_switch_plan {
+  int device = -1;
+  unsigned log_n = 0;
+  uint32_t element = 1;
+  size_t L = 0, K = 0, dnum = 0, max_batch = 0;
+  std::vector<uint64_t> host_q;
+  Buffers buf;
+  NttDevice d;
+  KsConst kc{};
+  KsConst* kc_dev = nullptr;
+  uint64_t *key = nullptr, *expanded = nullptr, *prod = nullptr, *in = nullptr, *out = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[4] = {};
+  praghip_timing timing{};
+  praghip_cleanup cleanup{};
+  bool closing = false;
+  void release() { release_all(device, buf, stream, ev, 4, cleanup, closing); }
+  ~praghip_switch_plan() { release(); }
+};
+
+namespace {
+int switch_failure(praghip_switch_plan* p, hipError_t e, const char* what) {
+  p->release();
+  return fail(PRAGHIP_E_DEVICE, std::string("E_SWITCH_HIP: ") + what + ": " + hipGetErrorString(e));
+}
+// Galois element validity (keyswitch/seal_adapter.cpp:35): odd and < 2N.
+bool galois_inverse(uint32_t g, unsigned log_n, uint32_t& ginv) {
+  const uint64_t two_n = 2ull << log_n;
+  if (!(g & 1) || g >= two_n) return false;
+  // (Z/2N)* has order N, so g^-1 = g^(N-1) mod 2N
+  uint64_t r = 1, b = g, e = (1ull << log_n) - 1;
+  for (; e; e >>= 1) {
+    if (e & 1) r = r * b % two_n;
+    b = b * b % two_n;
+  }
+  ginv = uint32_t(r);
+  return true;
+}
+int build_ks_const(const uint64_t* q, size_t L, size_t dnum, unsigned log_n, KsConst& kc) {
+  const size_t K = L + 1;
+  std::memset(&kc, 0, sizeof(kc));
+  kc.L = int(L);
+  kc.K = int(K);
+  kc.dnum = int(dnum);
+  kc.log_n = int(log_n);
+  const size_t base = L / dnum, extra = L % dnum;
+  for (size_t j = 0; j <= dnum; ++j) kc.dig_lo[j] = int(j * base + (j < extra ? j : extra));
+  for (size_t j = 0; j < dnum; ++j)
+    for (int i = kc.dig_lo[j]; i < kc.dig_lo[j + 1]; ++i) kc.digit_of[i] = int(j);
+  for (size_t t = 0; t < K; ++t) {
+    kc.q[t] = q[t];
+    const u128 ratio = (~(u128)0) / q[t];
+    kc.bar[t] = Barrett{q[t], uint64_t(ratio), uint64_t(ratio >> 64)};
+  }
+  for (size_t i = 0; i < L; ++i) {
+    const int j = kc.digit_of[i];
+    uint64_t h = 1;
+    for (int i2 = kc.dig_lo[j]; i2 < kc.dig_lo[j + 1]; ++i2)
+      if (size_t(i2) != i) h = mulmod(h, q[i2] % q[i], q[i]);
+    const uint64_t ih = invmod(h, q[i]);
+    kc.inv_hat[i] = Shoup{ih, shoup_q(ih, q[i])};
+    for (size_t t = 0; t < K; ++t) {
+      uint64_t ht = 1;
+      for (int i2 = kc.dig_lo[j]; i2 < kc.dig_lo[j + 1]; ++i2)
+        if (size_t(i2) != i) ht = mulmod(ht, q[i2] % q[t], q[t]);
+      kc.hat[i][t] = Shoup{ht, shoup_q(ht, q[t])};
+    }
+    const uint64_t p = q[L];
+    const uint64_t ip = invmod(p % q[i], q[i]);
+    kc.invp[i] = Shoup{ip, shoup_q(ip, q[i])};
+    kc.half_mod[i] = (p >> 1) % q[i];
+    kc.one_q[i] = shoup_q(1, q[i]);
+  }
+  return PRAGHIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes, uint32_t log_n, size_t dnum,
+                               const uint64_t* key, uint32_t element, size_t max_batch, praghip_switch_plan** plan) {
+  if (!plan || !q) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *plan = nullptr;
+  const size_t L = data_primes, K = L + 1;
+  if (log_n < 4 || log_n > 14 || L < 1 || K > size_t(kMaxKeyPrimes) || dnum < 1 || dnum > L || max_batch < 1)
+    return fail(PRAGHIP_E_SHAPE, "E_SWITCH_SHAPE");
+  uint32_t ginv = 1;
+  if (!galois_inverse(element, log_n, ginv)) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ELEMENT");
+  NttHost h;
+  if (int rc = build_ntt_host(q, K, log_n, nullptr, nullptr, nullptr, h)) return rc;
+  const size_t n = size_t(1) << log_n, key_words = dnum * 2 * K * n;
+  if (key)
+    for (size_t i = 0; i < key_words; ++i)
+      if (key[i] >= q[(i >> log_n) % K]) return fail(PRAGHIP_E_CANONICAL, "E_SWITCH_KEY_CANONICAL");
+  if (int rc = check_device(device)) return rc;
+  std::unique_ptr<praghip_switch_plan> p(new praghip_switch_plan);
+  p->device = device;
+  p->log_n = log_n;
+  p->element = element;
+  p->L = L;
+  p->K = K;
+  p->dnum = dnum;
+  p->max_batch = max_batch;
+  p->host_q.assign(q, q + K);
+  build_ks_const(q, L, dnum, log_n, p->kc);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+  for (auto& ev : p->ev)
+    if (e == hipSuccess) e = hipEventCreate(&ev);
+  if (e == hipSuccess) e = upload_ntt(h, log_n, p->buf, p->d, p->stream);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->kc_dev, sizeof(KsConst), false);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->kc_dev, &p->kc, sizeof(KsConst), hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess && key) e = p->buf.alloc((void**)&p->key, key_words * 8, true);
+  if (e == hipSuccess && key) e = hipMemcpyAsync(p->key, key, key_words * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->expanded, max_batch * dnum * K * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, max_batch * 2 * K * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->in, 2 * L * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->out, 2 * L * n * 8, true);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return switch_failure(p.get(), e, "create");
+  p->timing.device_bytes = p->buf.total_bytes();
+  p->timing.sensitive_bytes = p->buf.sensitive_bytes();
+  *plan = p.release();
+  return PRAGHIP_OK;
+}
+
+static hipError_t keyswitch_chunks(praghip_switch_plan* p, const uint64_t* in, uint64_t* out, size_t batch,
+                                   const uint64_t* keys, size_t key_stride, uint32_t ginv, hipStream_t s) {
+  const size_t n = size_t(1) << p->log_n, ct_words = 2 * p->L * n;
+  for (size_t b0 = 0; b0 < batch; b0 += p->max_batch) {
+    KsArgs a;
+    a.batch = std::min(p->max_batch, batch - b0);
+    a.in = in + b0 * ct_words;
+    a.out = out + b0 * ct_words;
+    a.key = keys + b0 * key_stride;
+    a.key_stride = key_stride;
+    a.expanded = p->expanded;
+    a.prod = p->prod;
+    a.galois_inv = ginv;
+    const hipError_t e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+int praghip_keyswitch(praghip_switch_plan* p, const uint64_t* input, uint64_t* output, size_t batch,
+                      const uint64_t* keys, size_t key_stride, uint32_t galois_elt, void* stream) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  if (batch && (!input || !output)) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (input == output && batch) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ALIAS");
+  if (!keys && !p->key) return fail(PRAGHIP_E_STATE, "E_SWITCH_NO_KEY");
+  uint32_t ginv = 1;
+  if (!galois_inverse(galois_elt, p->log_n, ginv)) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ELEMENT");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess)
+    e = keyswitch_chunks(p, input, output, batch, keys ? keys : p->key, keys ? key_stride : 0, ginv,
+                         pick(stream));
+  if (e != hipSuccess) return switch_failure(p, e, "keyswitch");
+  return PRAGHIP_OK;
+}
+
+int praghip_switch_apply(praghip_switch_plan* p, const uint64_t* input, uint64_t* output) {
+  if (!p || !input || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  if (!p->key) return fail(PRAGHIP_E_STATE, "E_SWITCH_NO_KEY");
+  const size_t n = size_t(1) << p->log_n, words = 2 * p->L * n;
+  for (size_t i = 0; i < words; ++i)
+    if (input[i] >= p->host_q[(i >> p->log_n) % p->L]) return fail(PRAGHIP_E_CANONICAL, "E_SWITCH_CIPHERTEXT");
+  uint32_t ginv = 1;
+  galois_inverse(p->element, p->log_n, ginv);
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  hipStream_t s = p->stream;
+  if (e == hipSuccess) e = hipEventRecord(p->ev[0], s);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->in, input, words * 8, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[1], s);
+  if (e == hipSuccess) e = keyswitch_chunks(p, p->in, p->out, 1, p->key, 0, ginv, s);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[2], s);
+  if (e == hipSuccess) e = hipMemcpyAsync(output, p->out, words * 8, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[3], s);
+  if (e == hipSuccess) e = hipEventSynchronize(p->ev[3]);
+  float t01 = 0, t12 = 0, t23 = 0;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t01, p->ev[0], p->ev[1]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&t12, p->ev[1], p->ev[2]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&t23, p->ev[2], p->ev[3]);
+  if (e != hipSuccess) {
+    std::memset(output, 0, words * 8);
+    return switch_failure(p, e, "apply");
+  }
+  p->timing.upload_ms = t01;
+  p->timing.kernel_ms = t12;
+  p->timing.download_ms = t23;
+  return PRAGHIP_OK;
+}
+
+int praghip_switch_sync(praghip_switch_plan* p) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return switch_failure(p, e, "sync");
+  return PRAGHIP_OK;
+}
+
+int praghip_switch_timing(const praghip_switch_plan* p, praghip_timing* out) {
+  if (!p || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *out = p->timing;
+  return PRAGHIP_OK;
+}
+
+int praghip_switch_close(praghip_switch_plan* p, praghip_cleanup* out) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  p->release();
+  if (out) *out = p->cleanup;
+  return PRAGHIP_OK;
+}
+
+void praghip_switch_destroy(praghip_switch_plan* p) { delete p; }
+
+// ================================================================ share GEMM
+int praghip_share_gemm(int device, const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
+                       size_t m, size_t k, size_t n, int mask_bits, void* stream) {
+  if (m == 0 || n == 0) return PRAGHIP_OK;
+  if (!x || !w || !y) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (w_bits != 8 && w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
+  if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
+  if (k >= (1u << 17) || m >= (1u << 31) || n >= (1u << 31)) return fail(PRAGHIP_E_SHAPE, "E_SHARE_SHAPE");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess)
+    e = launch_share_gemm(x, w, w_bits, shifts, y, int(m), int(k), int(n), mask_bits, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_SHARE_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
+}  // extern "C"
+
+// ========================================================= synthetic inputs
+extern "C" {
+
+int praghip_fill_residues(int device, uint64_t* data, size_t limbs, uint32_t log_n, const uint64_t* q,
+                          size_t primes, uint64_t seed, void* stream) {
+  if (!q || (!data && limbs)) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (primes < 1 || primes > size_t(kMaxKeyPrimes) || log_n > 20) return fail(PRAGHIP_E_SHAPE, "E_FILL_SHAPE");
+  PrimeList pl{};
+  for (size_t i = 0; i < primes; ++i) pl.q[i] = q[i];
+  pl.count = int(primes);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess)
+    e = launch_fill_residues(data, limbs << log_n, int(log_n), pl, seed, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_FILL_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
+int praghip_fill_u64(int device, uint64_t* data, size_t count, uint64_t seed, void* stream) {
+  if (!data && count) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_fill_u64(data, count, seed, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_FILL_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
+int praghip_fill_i8(int device, int8_t* data, size_t count, uint64_t seed, void* stream) {
+  if (!data && count) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_fill_i8(data, count, seed, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_FILL_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
+}  // extern "C"

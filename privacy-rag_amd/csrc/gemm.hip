@@ -1,0 +1,220 @@
+// Party-local share GEMM over Z_2^64 on the i8 matrix cores of gfx950.
+//
+//   y[m][n] = ((sum_k x[m][k] * w[n][k]) << s_n)  mod 2^mask_bits
+//
+// (bfv_matrix.inc:101-105 / 156-160 / 177-182: the reference runs this as a
+// scalar triple loop on the protocol thread.)
+//
+// Exactness.  Each u64 share is split into its 8 bytes b_d and re-centred as
+// signed digits a_d = b_d - 128 (one XOR with 0x80 per byte), so that
+//   x = sum_d (a_d + 128) 256^d
+//   sum_k x w = sum_d 256^d (sum_k a_d w)  +  0x8080808080808080 * sum_k w   (mod 2^64).
+// Every digit product a_d * w fits i8 x i8, and each column of partial sums
+// fits the i32 accumulator (|a_d w| <= 2^14, K < 2^17).  int32 weights in
+// [-0x808080, 0x7F7F7F] (the reference f12 domain is |w| <= 2^20) are split
+// into three balanced signed bytes w = sum_e w_e 256^e and run as one pass per
+// weight byte, each pass shifting its contribution by 8e and accumulating
+// mod 2^64.
+//
+// Tiling.  One MFMA v_mfma_i32_32x32x32_i8 covers 32 "digit rows" = 4 share
+// rows x 8 digits, ordered so that the 16 accumulator registers of a lane hold
+// all 8 digits of 2 share rows for its column (32x32 accumulator layout: lane l,
+// register r -> column l%32, row 8(r/4) + 4(l/32) + r%4).  The digit sum is
+// therefore formed in registers with no cross-lane traffic.  A workgroup of 4
+// waves computes 32 share rows x 128 columns; each wave 16 rows x 64 columns
+// (8 MFMAs per 32-wide K step).  Shares are staged in LDS as 8 digit planes
+// (byte transpose with v_perm), weights as int8 rows; both with an 80-byte row
+// pitch so the 16-byte operand reads are bank-conflict free.
+#include "kernels.hpp"
+
+namespace praghip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 32, kBN = 128, kBK = 64, kPitch = 80, kThreads = 256;
+
+// o_d byte e = a_e byte d, for four dwords a0..a3.
+__device__ __forceinline__ void transpose4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t& o0,
+                                           uint32_t& o1, uint32_t& o2, uint32_t& o3) {
+  const uint32_t p0 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
+  const uint32_t p1 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+  const uint32_t p2 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+  const uint32_t p3 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+  o0 = __builtin_amdgcn_perm(p2, p0, 0x05040100u);
+  o1 = __builtin_amdgcn_perm(p2, p0, 0x07060302u);
+  o2 = __builtin_amdgcn_perm(p3, p1, 0x05040100u);
+  o3 = __builtin_amdgcn_perm(p3, p1, 0x07060302u);
+}
+
+// Balanced signed byte e (e < 3) of a weight in [-0x808080, 0x7F7F7F].
+__device__ __forceinline__ int weight_digit(int w, int e) {
+  for (int i = 0; i < e; ++i) {
+    const int lo = (int)(int8_t)(w & 0xff);
+    w = (w - lo) >> 8;
+  }
+  return (int)(int8_t)(w & 0xff);
+}
+
+template <int WB>
+__global__ void __launch_bounds__(kThreads)
+    share_gemm_kernel(const uint64_t* __restrict__ x, const void* __restrict__ wv, const int8_t* __restrict__ shifts,
+                      uint64_t* __restrict__ y, int M, int K, int N, uint64_t mask, int wdigit, int accumulate) {
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM][kPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t w_lds[kBN][kPitch];
+  __shared__ int csum[kThreads];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+
+  // share-tile loader: row ar, 8 consecutive k from ak
+  const int ar = t >> 3, ak = (t & 7) * 8;
+  // weight-tile loader: row wr, 32 consecutive k from wk
+  const int wr = t >> 1, wk = (t & 1) * 32;
+  int colsum = 0;
+
+  // MFMA operand coordinates of this lane
+  const int i = lane & 31, khalf = lane >> 5;
+  const int a_row_in_block = 2 * ((i >> 2) & 1) + (i >> 4);
+  const int a_digit = 4 * ((i >> 3) & 1) + (i & 3);
+
+  v16i acc[4][2];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16i{0};
+
+  const bool x_row_ok = (m0 + ar) < M;
+  const bool w_row_ok = (n0 + wr) < N;
+  const uint64_t* xrow = x + size_t(m0 + ar) * K;
+
+  for (int k0 = 0; k0 < K; k0 += kBK) {
+    // ---- shares -> 8 offset-binary digit planes
+    uint32_t d[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int kk = k0 + ak + e;
+      const uint64_t v = (x_row_ok && kk < K) ? xrow[kk] : 0;
+      d[2 * e] = uint32_t(v) ^ 0x80808080u;
+      d[2 * e + 1] = uint32_t(v >> 32) ^ 0x80808080u;
+    }
+    uint32_t o[4][4];
+    transpose4(d[0], d[2], d[4], d[6], o[0][0], o[0][1], o[0][2], o[0][3]);      // digits 0-3, k 0-3
+    transpose4(d[8], d[10], d[12], d[14], o[1][0], o[1][1], o[1][2], o[1][3]);   // digits 0-3, k 4-7
+    transpose4(d[1], d[3], d[5], d[7], o[2][0], o[2][1], o[2][2], o[2][3]);      // digits 4-7, k 0-3
+    transpose4(d[9], d[11], d[13], d[15], o[3][0], o[3][1], o[3][2], o[3][3]);   // digits 4-7, k 4-7
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg) {
+      *reinterpret_cast<uint2*>(&a_lds[dg][ar][ak]) = make_uint2(o[0][dg], o[1][dg]);
+      *reinterpret_cast<uint2*>(&a_lds[dg + 4][ar][ak]) = make_uint2(o[2][dg], o[3][dg]);
+    }
+    // ---- weights (digit `wdigit` of each) -> int8 rows
+    uint32_t wb[8];
+    if (WB == 8) {
+      const int8_t* wrow = static_cast<const int8_t*>(wv) + size_t(n0 + wr) * K;
+      const int kk = k0 + wk;
+      if (w_row_ok && kk + 32 <= K && ((K & 15) == 0)) {
+        const uint4 a = *reinterpret_cast<const uint4*>(wrow + kk);
+        const uint4 b = *reinterpret_cast<const uint4*>(wrow + kk + 16);
+        wb[0] = a.x; wb[1] = a.y; wb[2] = a.z; wb[3] = a.w;
+        wb[4] = b.x; wb[5] = b.y; wb[6] = b.z; wb[7] = b.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) {
+            const int kq = kk + 4 * q + bb;
+            const uint32_t byte = (w_row_ok && kq < K) ? uint8_t(wrow[kq]) : 0u;
+            word |= byte << (8 * bb);
+          }
+          wb[q] = word;
+        }
+      }
+    } else {
+      const int32_t* wrow = static_cast<const int32_t*>(wv) + size_t(n0 + wr) * K;
+      const int kk = k0 + wk;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const int kq = kk + 4 * q + bb;
+          const int wvv = (w_row_ok && kq < K) ? wrow[kq] : 0;
+          word |= uint32_t(uint8_t(weight_digit(wvv, wdigit))) << (8 * bb);
+        }
+        wb[q] = word;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) colsum = __builtin_amdgcn_sdot4(int(wb[q]), 0x01010101, colsum, false);
+    *reinterpret_cast<uint4*>(&w_lds[wr][wk]) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+    *reinterpret_cast<uint4*>(&w_lds[wr][wk + 16]) = make_uint4(wb[4], wb[5], wb[6], wb[7]);
+    __syncthreads();
+
+    // ---- MFMA over the two 32-wide K steps
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      const int kb = ks * 32 + khalf * 16;
+      v4i bop[2];
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) bop[cb] = *reinterpret_cast<const v4i*>(&w_lds[wn * 64 + cb * 32 + i][kb]);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        const v4i aop = *reinterpret_cast<const v4i*>(&a_lds[a_digit][wm * 16 + rb * 4 + a_row_in_block][kb]);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          acc[rb][cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[cb], acc[rb][cb], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: column sums, digit recombination, shift, mask
+  csum[t] = colsum;
+  __syncthreads();
+  const int shift_e = 8 * wdigit;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int cl = wn * 64 + cb * 32 + i;
+    const int col = n0 + cl;
+    if (col >= N) continue;
+    const int64_t s_n = int64_t(csum[2 * cl]) + int64_t(csum[2 * cl + 1]);
+    const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
+    const int sh = shift_e + (shifts ? int(shifts[col]) : 0);
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int row = m0 + wm * 16 + rb * 4 + 2 * khalf + a;
+        if (row >= M) continue;
+        uint64_t v = corr;
+#pragma unroll
+        for (int dg = 0; dg < 8; ++dg) v += uint64_t(int64_t(acc[rb][cb][8 * a + dg])) << (8 * dg);
+        v = sh < 64 ? (v << sh) : 0;
+        uint64_t* dst = y + size_t(row) * N + col;
+        if (accumulate) v += *dst;
+        *dst = v & mask;
+      }
+    }
+  }
+}
+
+hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
+                             int M, int K, int N, int mask_bits, hipStream_t s) {
+  const uint64_t mask = mask_bits >= 64 ? ~0ull : ((1ull << mask_bits) - 1);
+  const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(kThreads);
+  if (w_bits == 8) {
+    hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, 0, 0);
+    return hipGetLastError();
+  }
+  for (int e = 0; e < 3; ++e) {
+    hipLaunchKernelGGL((share_gemm_kernel<32>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, e, e > 0);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+}  // namespace praghip

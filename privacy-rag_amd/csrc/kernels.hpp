@@ -1,0 +1,67 @@
+// Internal interface between the C ABI layer (api.cpp) and the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "ntt_core.hpp"
+
+namespace praghip {
+
+// Device-resident NTT tables of one prime set.
+struct NttDevice {
+  int log_n = 0, P = 0;
+  NttPrime* primes = nullptr;        // [P]
+  ulonglong2* tw_fwd_u = nullptr;    // [P][N] (w, floor(w 2^64/q))
+  ulonglong2* tw_inv_u = nullptr;    // [P][N]
+  double2* tw_fwd_f = nullptr;       // [P][N] (w, w/q) for q < 2^50
+  double2* tw_inv_f = nullptr;       // [P][N]
+};
+
+hipError_t launch_ntt(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d, hipStream_t s);
+hipError_t launch_dyadic_shoup(uint64_t* data, const ulonglong2* key, const NttDevice& d, size_t words,
+                               hipStream_t s);
+
+// Keyswitch constants (device).  K = L + 1 key primes; prime L is the special
+// prime p.  Digit j covers data primes [dig_lo[j], dig_lo[j+1]).
+constexpr int kMaxKeyPrimes = 16;
+struct KsConst {
+  int L, K, dnum, log_n;
+  int dig_lo[kMaxKeyPrimes + 1];
+  int digit_of[kMaxKeyPrimes];           // data prime -> digit
+  uint64_t q[kMaxKeyPrimes];
+  Barrett bar[kMaxKeyPrimes];            // Barrett-128 ratios (product kernel)
+  Shoup inv_hat[kMaxKeyPrimes];          // ((Q_j/q_i) mod q_i)^-1, mod q_i
+  Shoup hat[kMaxKeyPrimes][kMaxKeyPrimes];  // (Q_j/q_i) mod q_t, mod q_t   [i][t]
+  Shoup invp[kMaxKeyPrimes];             // p^-1 mod q_i
+  uint64_t half_mod[kMaxKeyPrimes];      // floor(p/2) mod q_i
+  uint64_t one_q[kMaxKeyPrimes];         // floor(2^64 / q_i): Shoup constant of 1
+};
+
+struct KsArgs {
+  const uint64_t* in;    // [batch][2][L][N] coefficient form
+  uint64_t* out;         // [batch][2][L][N]
+  const uint64_t* key;   // [dnum][2][K][N] NTT form, + b * key_stride
+  size_t key_stride;     // words between consecutive ciphertexts' keys (0 = shared)
+  uint64_t* expanded;    // scratch [batch][dnum][K][N]
+  uint64_t* prod;        // scratch [batch][2][K][N]
+  size_t batch;
+  uint32_t galois_inv;   // g^-1 mod 2N (1 = identity)
+};
+
+// Prime list passed by value to the fill kernel.
+struct PrimeList {
+  uint64_t q[kMaxKeyPrimes];
+  int count;
+};
+hipError_t launch_fill_residues(uint64_t* out, size_t words, int log_n, const PrimeList& q, uint64_t seed,
+                                hipStream_t s);
+hipError_t launch_fill_u64(uint64_t* out, size_t count, uint64_t seed, hipStream_t s);
+hipError_t launch_fill_i8(int8_t* out, size_t count, uint64_t seed, hipStream_t s);
+
+hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
+                            hipStream_t s);
+
+}  // namespace praghip

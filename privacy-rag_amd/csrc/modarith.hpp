@@ -1,0 +1,96 @@
+// Modular arithmetic shared by the gfx950 kernels (device) and the plan
+// builders (host).  All moduli are odd primes q < 2^62.
+//
+// Integer path: Shoup multiplication by a precomputed constant (the operand /
+// quotient pairs of SEAL's MultiplyUIntModOperand, used by the reference at
+// switch.cu:13-16), in Harvey's lazy form: for any a < 2^64 and w < q,
+//   a*w - mulhi(a, floor(w*2^64/q))*q  lies in [0, 2q).
+// Barrett-128 for products of two runtime residues (switch.cu:30-45).
+//
+// Float path (q < 2^50): residues held as exact integers in IEEE doubles.  The
+// product a*w is split error-free into hi + lo with one FMA, the quotient is
+// rounded with the 1.5*2^52 shifter, and the remainder hi - c*q is exact
+// because it is an integer below 2^53.  Results are centred: |r| <= 0.76 q for
+// |a| <= 2q, w < q.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define PH_HD __host__ __device__ __forceinline__
+
+namespace praghip {
+
+PH_HD uint64_t mulhi64(uint64_t a, uint64_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __umul64hi(a, b);
+#else
+  return (uint64_t)(((unsigned __int128)a * b) >> 64);
+#endif
+}
+
+// ------------------------------------------------------------------ integer
+struct Shoup {
+  uint64_t w, wq;  // operand, floor(operand * 2^64 / q)
+};
+
+// a*w mod q in [0, 2q) for any a < 2^64.
+PH_HD uint64_t mul_shoup_lazy(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
+  return a * w - mulhi64(a, wq) * q;
+}
+PH_HD uint64_t mul_shoup(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
+  uint64_t r = mul_shoup_lazy(a, w, wq, q);
+  return r >= q ? r - q : r;
+}
+PH_HD uint64_t add_mod(uint64_t a, uint64_t b, uint64_t q) {
+  uint64_t x = a + b;
+  return x >= q ? x - q : x;
+}
+PH_HD uint64_t sub_mod(uint64_t a, uint64_t b, uint64_t q) {
+  uint64_t x = a + q - b;
+  return x >= q ? x - q : x;
+}
+
+// SEAL barrett_reduce_128 applied to a*b with ratio floor((2^128-1)/q) = (r0, r1).
+struct Barrett {
+  uint64_t q, r0, r1;
+};
+PH_HD uint64_t mul_barrett(uint64_t a, uint64_t b, const Barrett m) {
+  const uint64_t lo = a * b, hi = mulhi64(a, b);
+  const uint64_t carry0 = mulhi64(lo, m.r0);
+  const uint64_t round1 = lo * m.r1;
+  const uint64_t tmp = round1 + carry0;
+  const uint64_t high1 = mulhi64(lo, m.r1) + (tmp < round1);
+  const uint64_t round2 = hi * m.r0;
+  const uint64_t next = tmp + round2;
+  const uint64_t high2 = mulhi64(hi, m.r0) + (next < tmp);
+  const uint64_t quotient = hi * m.r1 + high1 + high2;
+  const uint64_t rem = lo - quotient * m.q;
+  return rem >= m.q ? rem - m.q : rem;
+}
+
+// -------------------------------------------------------------------- float
+constexpr double kShifter = 6755399441055744.0;  // 1.5 * 2^52: x + S - S = rint(x) for |x| < 2^51
+
+struct ShoupF {
+  double w, wq;  // operand (exact integer), operand / q
+};
+
+// a*w mod q, centred: |r| <= 0.76 q for |a| <= 2q (q < 2^50, w < q).
+PH_HD double mul_f64(double a, double w, double wq, double q) {
+  const double hi = a * w;
+  const double lo = __builtin_fma(a, w, -hi);
+  const double c = __builtin_fma(a, wq, kShifter) - kShifter;
+  return __builtin_fma(-c, q, hi) + lo;
+}
+// x mod q, centred to |r| <= q/2 + 1 for |x| < 2^51 (qinv = 1/q).
+PH_HD double reduce_f64(double x, double q, double qinv) {
+  const double c = __builtin_fma(x, qinv, kShifter) - kShifter;
+  return __builtin_fma(-c, q, x);
+}
+// centred residue (|x| < 2q) -> canonical [0, q)
+PH_HD double canon_f64(double x, double q) {
+  x = x < 0.0 ? x + q : x;
+  return x >= q ? x - q : x;
+}
+
+}  // namespace praghip

@@ -1,0 +1,23 @@
+"""praghip: MI355X (gfx950) backend for the BFV polynomial engine and the
+party-local Z_2^64 share GEMM of HaoR265/privacy-rag.
+
+Python mirror of the reference's GPU backend classes over the C ABI of
+libpraghip.so:
+
+* :class:`NttBatch`  - prag::experimental::ntt::NttBatch (ntt.hpp:22-40)
+* :class:`Switch`    - prag::experimental_full_switch::Switch (switch.hpp:12-28)
+* :func:`share_gemm` - the party-local share GEMM (bfv_matrix.inc:101-105),
+  offered as a LocalShares operation (local_shares.hpp:22-32)
+
+Device data is handed over as torch tensors on the GPU (int64 or uint64 with
+u64 bit patterns); torch is used only for memory and streams.
+"""
+from ._lib import Cleanup, PraghipError, Timing, check, lib  # noqa: F401
+from .ntt import NttBatch, ntt_tables  # noqa: F401
+from .keyswitch import Switch  # noqa: F401
+from .shares import share_gemm  # noqa: F401
+from . import synth  # noqa: F401
+
+
+def device_count() -> int:
+    return int(lib().praghip_device_count())

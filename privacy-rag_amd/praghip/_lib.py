@@ -1,0 +1,89 @@
+"""ctypes binding of libpraghip.so (include/praghip.h).
+
+The library is built in-tree by ``praghip._build.build()``.  There is no
+fallback: importing the package without the built library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libpraghip.so")
+
+OK, E_SHAPE, E_CANONICAL, E_CONTEXT, E_CLOSED, E_DEVICE, E_ARGUMENT, E_STATE = range(8)
+
+
+class PraghipError(RuntimeError):
+    def __init__(self, code: int, text: str):
+        super().__init__(f"{text} (status {code})")
+        self.code = code
+        self.text = text
+
+
+class Cleanup(ctypes.Structure):
+    """Cleanup{first_cuda_error, wipe_synchronized_bytes, freed_bytes, closed} (ntt.hpp:15-19)."""
+    _fields_ = [("first_hip_error", ctypes.c_int32), ("closed", ctypes.c_int32),
+                ("wipe_synchronized_bytes", ctypes.c_uint64), ("freed_bytes", ctypes.c_uint64)]
+
+
+class Timing(ctypes.Structure):
+    _fields_ = [("upload_ms", ctypes.c_double), ("kernel_ms", ctypes.c_double), ("download_ms", ctypes.c_double),
+                ("device_bytes", ctypes.c_uint64), ("sensitive_bytes", ctypes.c_uint64)]
+
+
+vp, sz, u32, u64, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+pp = ctypes.POINTER(ctypes.c_void_p)
+
+SIGNATURES = {
+    "praghip_last_error": (ctypes.c_char_p, []),
+    "praghip_version": (i32, []),
+    "praghip_device_count": (i32, []),
+    "praghip_ntt_tables": (i32, [u64, u32, vp, vp, vp, vp]),
+    "praghip_ntt_plan_create": (i32, [i32, vp, sz, u32, vp, vp, vp, sz, pp]),
+    "praghip_ntt_forward": (i32, [vp, vp, sz, vp]),
+    "praghip_ntt_inverse": (i32, [vp, vp, sz, vp]),
+    "praghip_ntt_transform": (i32, [vp, vp, vp, i32]),
+    "praghip_ntt_bind_client_key": (i32, [vp, vp]),
+    "praghip_ntt_client_phase": (i32, [vp, vp, vp]),
+    "praghip_ntt_sync": (i32, [vp]),
+    "praghip_ntt_timing": (i32, [vp, ctypes.POINTER(Timing)]),
+    "praghip_ntt_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
+    "praghip_ntt_destroy": (None, [vp]),
+    "praghip_switch_plan_create": (i32, [i32, vp, sz, u32, sz, vp, u32, sz, pp]),
+    "praghip_switch_apply": (i32, [vp, vp, vp]),
+    "praghip_keyswitch": (i32, [vp, vp, vp, sz, vp, sz, u32, vp]),
+    "praghip_switch_sync": (i32, [vp]),
+    "praghip_switch_timing": (i32, [vp, ctypes.POINTER(Timing)]),
+    "praghip_switch_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
+    "praghip_switch_destroy": (None, [vp]),
+    "praghip_share_gemm": (i32, [i32, vp, vp, i32, vp, vp, sz, sz, sz, i32, vp]),
+    "praghip_fill_residues": (i32, [i32, vp, sz, u32, vp, sz, u64, vp]),
+    "praghip_fill_u64": (i32, [i32, vp, sz, u64, vp]),
+    "praghip_fill_i8": (i32, [i32, vp, sz, u64, vp]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def shape_error(text: str) -> PraghipError:
+    return PraghipError(E_SHAPE, text)
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise PraghipError(rc, lib().praghip_last_error().decode())

@@ -16,3 +16,29 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def golden_dir():
     return os.path.join(ROOT, "tests", "golden")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """torch device handle for the -m gpu tests (they only run on the GPU box)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    import praghip
+    assert praghip.device_count() >= 1, "praghip sees no gfx950 device"
+    return torch.device("cuda:0")
+
+
+def to_dev(a, device="cuda:0"):
+    import numpy as np
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint64:
+        a = a.view(np.int64)
+    return torch.from_numpy(a).to(device)
+
+
+def from_dev(t):
+    import numpy as np
+    a = t.detach().cpu().numpy()
+    return a.view(np.uint64) if a.dtype == np.int64 else a

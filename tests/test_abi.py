@@ -1,0 +1,90 @@
+"""C-ABI boundary checks that run without a GPU: the library loads, exports
+every symbol include/praghip.h declares, its host-side table builder agrees
+with the oracle and the closed form, and argument validation rejects bad
+plans before any device call."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import closed_form as cf
+import oracle
+import praghip
+from praghip import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    with open(os.path.join(ROOT, "include", "praghip.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(praghip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    names = header_functions()
+    assert len(names) >= 20
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in names:
+        assert hasattr(L, name), name
+    # the Python binding declares a signature for every exported entry point
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_library_links_no_oracle():
+    with open(_lib.LIB_PATH, "rb") as f:
+        blob = f.read()
+    assert b"orc_" not in blob and b"liboracle" not in blob
+
+
+@pytest.mark.parametrize("log_n", [4, 10, 12, 14])
+def test_tables_match_oracle(log_n):
+    n = 1 << log_n
+    for q in (cf.LOCKED_PRIMES[0], cf.LOCKED_PRIMES[6], cf.primes_below(50, n, 1)[0], cf.primes_below(54, n, 1)[0]):
+        f, i, ninv, psi = praghip.ntt_tables(q, log_n)
+        of, oi, on = oracle.ntt_tables(q, log_n)
+        assert psi == oracle.minimal_root(q, n)
+        np.testing.assert_array_equal(f, of)
+        np.testing.assert_array_equal(i, oi)
+        np.testing.assert_array_equal(ninv, on)
+
+
+def test_locked_psi_values(golden_dir):
+    import json
+    with open(os.path.join(golden_dir, "primes.json")) as fh:
+        psis = [int(x) for x in json.load(fh)["psi_16384"]]
+    for q, want in zip(cf.LOCKED_PRIMES, psis):
+        assert praghip.ntt_tables(q, 14)[3] == want
+
+
+def test_plan_validation_before_device():
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.NttBatch([1152921504599080963], 14)  # not prime
+    assert e.value.code == _lib.E_CONTEXT and "E_NTT_CONTEXT" in e.value.text
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.NttBatch([cf.LOCKED_PRIMES[0]], 15)
+    assert e.value.code == _lib.E_SHAPE
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.NttBatch([101], 4)  # 101 != 1 mod 32
+    assert e.value.code == _lib.E_CONTEXT
+    f, i, n, _ = praghip.ntt_tables(cf.LOCKED_PRIMES[1], 10)
+    f[5, 1] ^= 1  # corrupted quotient
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.NttBatch([cf.LOCKED_PRIMES[1]], 10, tables=(f[None], i[None], n[None]))
+    assert e.value.code == _lib.E_CONTEXT
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.Switch(cf.LOCKED_PRIMES, 14, dnum=7)
+    assert e.value.code == _lib.E_SHAPE
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.Switch(cf.LOCKED_PRIMES, 14, dnum=6, element=4)
+    assert e.value.code == _lib.E_ARGUMENT
+
+
+def test_no_device_here_is_reported():
+    if praghip.device_count() > 0:
+        pytest.skip("a GPU is present")
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.NttBatch([cf.LOCKED_PRIMES[0]], 14)
+    assert e.value.code == _lib.E_DEVICE and "E_GFX950_REQUIRED" in e.value.text

@@ -1,0 +1,75 @@
+"""GPU parity of the party-local share GEMM against the oracle and fixtures."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import praghip
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(x, w, shifts=None, mask_bits=64):
+    import torch
+    tx = to_dev(x)
+    tw = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+    ts = None if shifts is None else torch.from_numpy(np.ascontiguousarray(shifts, dtype=np.int8)).cuda()
+    y = praghip.share_gemm(tx, tw, shifts=ts, mask_bits=mask_bits)
+    torch.cuda.synchronize()
+    return from_dev(y)
+
+
+def test_gemm_golden(gpu, golden_dir):
+    data = np.load(os.path.join(golden_dir, "gemm_small.npz"))
+    for name in ("i8_a", "i8_shift59", "i32_a", "i32_shift59"):
+        sh = data[name + "_shift"] if name + "_shift" in data.files else None
+        got = _run(data[name + "_x"], data[name + "_w"], sh, int(data[name + "_mask"][0]))
+        np.testing.assert_array_equal(got, data[name + "_y"], err_msg=name)
+    yc = _run(data["probe_client"], data["probe_weight"], None, 59)
+    ys = _run(data["probe_server"], data["probe_weight"], None, 59)
+    np.testing.assert_array_equal((yc + ys) & np.uint64((1 << 59) - 1), data["probe_plain"])
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (5, 7, 3), (33, 65, 129), (64, 128, 256), (100, 1000, 300),
+                                   (31, 2048, 127), (512, 64, 128)])
+@pytest.mark.parametrize("wdt", ["i8", "i32"])
+def test_gemm_ragged_vs_oracle(gpu, m, k, n, wdt):
+    print(f"[gemm] m={m} k={k} n={n} {wdt}", flush=True)
+    x = oracle.fill_u64(m * k, 1000 + m).reshape(m, k)
+    if wdt == "i8":
+        w = oracle.fill_i8(n * k, 2000 + n).reshape(n, k)
+    else:
+        w = (oracle.fill_u64(n * k, 3000 + n) % np.uint64(1 << 21)).astype(np.int64) - (1 << 20)
+        w = w.astype(np.int32).reshape(n, k)
+    sh = oracle.fill_shift(n, 4000 + k)
+    for shifts, mask in ((None, 64), (sh, 59)):
+        want = oracle.share_gemm(x, w, shifts, mask)
+        np.testing.assert_array_equal(_run(x, w, shifts, mask), want)
+
+
+def test_gemm_extreme_values(gpu):
+    m, k, n = 40, 256, 160
+    x = np.full((m, k), np.uint64((1 << 64) - 1))
+    x[1] = 0
+    x[2] = np.uint64(1 << 63)
+    x[3] = np.uint64(0x8080808080808080)
+    w = np.full((n, k), -127, dtype=np.int8)
+    w[1] = 127
+    w[2] = -128
+    w[3] = 0
+    np.testing.assert_array_equal(_run(x, w), oracle.share_gemm(x, w))
+    w32 = np.full((n, k), -(1 << 20), dtype=np.int32)
+    w32[1] = 1 << 20
+    w32[2] = 0x7F7F7F  # largest weight with three balanced signed bytes
+    w32[3] = -0x808080  # smallest
+    np.testing.assert_array_equal(_run(x, w32), oracle.share_gemm(x, w32))
+
+
+def test_gemm_c4_full_shape(gpu):
+    """C4: activation shares u64 [512 x 1024] times int8 [3072 x 1024] -> [512 x 3072] mod 2^64."""
+    m, k, n = 512, 1024, 3072
+    x = oracle.fill_u64(m * k, 0x5052414700000004).reshape(m, k)
+    w = oracle.fill_i8(n * k, 0x5052414700000104).reshape(n, k)
+    np.testing.assert_array_equal(_run(x, w), oracle.share_gemm(x, w))

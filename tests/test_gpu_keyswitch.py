@@ -1,0 +1,107 @@
+"""GPU parity of the batched keyswitch against the oracle and the closed-form fixtures."""
+import os
+
+import numpy as np
+import pytest
+
+import closed_form as cf
+import oracle
+import praghip
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+C3 = cf.primes_below(50, 16384, 6) + cf.primes_below(60, 16384, 1)
+
+
+def test_keyswitch_golden_fixtures(gpu, golden_dir):
+    data = np.load(os.path.join(golden_dir, "keyswitch_small.npz"))
+    tags = sorted({k.rsplit("_", 1)[0] for k in data.files})
+    for tag in tags:
+        q = [int(x) for x in data[tag + "_q"]]
+        dnum, g, n = (int(v) for v in data[tag + "_meta"])
+        print(f"[ks-golden] {tag}", flush=True)
+        sw = praghip.Switch(q, n.bit_length() - 1, dnum, key=data[tag + "_key"], element=g)
+        np.testing.assert_array_equal(sw.apply(data[tag + "_ct"]), data[tag + "_out"], err_msg=tag)
+
+
+@pytest.mark.parametrize("element", [1, 3, (1 << 10) + 1, 2 * 16384 - 1])
+def test_keyswitch_locked_reference_dnum6(gpu, element):
+    """The reference configuration: 7 locked 60-bit primes, one digit per data prime."""
+    q, n, L, dnum, batch = cf.LOCKED_PRIMES, 16384, 6, 6, 2
+    print(f"[ks] locked dnum=6 element={element}", flush=True)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000203).reshape(batch, 2, L, n)
+    key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 0x5052414700010203).reshape(dnum, 2, L + 1, n)
+    want = oracle.keyswitch(ct, key, q, dnum, 14, element)
+    sw = praghip.Switch(q, 14, dnum, key=key, element=element, max_batch=batch)
+    tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
+    sw.keyswitch(tin, tout, galois=element)
+    np.testing.assert_array_equal(from_dev(tout), want)
+    # host Switch::apply path (upload, Galois(element), keyswitch, download)
+    np.testing.assert_array_equal(sw.apply(ct[1]), want[1])
+
+
+@pytest.mark.parametrize("dnum", [3, 2, 6])
+def test_keyswitch_c3_modup_per_ciphertext_keys(gpu, dnum):
+    """C3 shape: 6 data primes ~50 bits + 60-bit special prime, dnum digits, one key per ciphertext."""
+    q, n, L, batch = C3, 16384, 6, 3
+    print(f"[ks] c3 dnum={dnum}", flush=True)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000303).reshape(batch, 2, L, n)
+    keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x5052414700010303).reshape(
+        batch, dnum, 2, L + 1, n)
+    want = oracle.keyswitch(ct, keys, q, dnum, 14, 5, per_ct_keys=True)
+    sw = praghip.Switch(q, 14, dnum, max_batch=2)  # batch 3 runs as two chunks
+    tin, tout, tk = to_dev(ct), to_dev(np.zeros_like(ct)), to_dev(keys)
+    sw.keyswitch(tin, tout, keys=tk, key_stride=sw.key_words, galois=5)
+    np.testing.assert_array_equal(from_dev(tout), want)
+    # shared key (key_stride 0) on the same inputs
+    want0 = oracle.keyswitch(ct, keys[0], q, dnum, 14, 1)
+    sw.keyswitch(tin, tout, keys=tk, key_stride=0, galois=1)
+    np.testing.assert_array_equal(from_dev(tout), want0)
+
+
+def test_keyswitch_edge_inputs(gpu):
+    """Zero ciphertext, all q-1, and the check_switch.cpp:20 patterns in c1."""
+    q, n, L, dnum = C3, 16384, 6, 3
+    key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 77).reshape(dnum, 2, L + 1, n)
+    sw = praghip.Switch(q, 14, dnum, key=key, element=3)
+    qs = np.array(q[:L], dtype=np.uint64)[:, None]
+    cases = {
+        "zero": np.zeros((2, L, n), dtype=np.uint64),
+        "max": np.broadcast_to(qs - np.uint64(1), (2, L, n)).copy(),
+        "pattern": np.stack([np.zeros((L, n), dtype=np.uint64),
+                             (((np.arange(n, dtype=np.uint64) * np.uint64(7919) + np.uint64(123456))
+                               & np.uint64((1 << 59) - 1))[None, :] % qs)]),
+    }
+    for name, ct in cases.items():
+        want = oracle.keyswitch(ct[None], key, q, dnum, 14, 3)[0]
+        np.testing.assert_array_equal(sw.apply(ct), want, err_msg=name)
+
+
+def test_switch_errors_and_cleanup(gpu):
+    q, n, L, dnum = cf.LOCKED_PRIMES, 16384, 6, 6
+    key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 1).reshape(dnum, 2, L + 1, n)
+    sw = praghip.Switch(q, 14, dnum, key=key, element=1)
+    ct = oracle.fill_residues(2 * L, n, q[:L], 2).reshape(2, L, n)
+    bad = ct.copy()
+    bad[1, 2, 5] = np.uint64(q[2])
+    with pytest.raises(praghip.PraghipError) as e:
+        sw.apply(bad)
+    assert "E_SWITCH_CIPHERTEXT" in e.value.text
+    tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
+    with pytest.raises(praghip.PraghipError) as e:
+        sw.keyswitch(tin, tout, galois=2)
+    assert "E_SWITCH_ELEMENT" in e.value.text
+    t = sw.timing()
+    c = sw.close()
+    assert c.closed and c.first_hip_error == 0
+    assert c.wipe_synchronized_bytes == c.freed_bytes == t.sensitive_bytes > 0
+    assert sw.close().freed_bytes == t.sensitive_bytes
+    with pytest.raises(praghip.PraghipError) as e:
+        sw.apply(ct)
+    assert "E_SWITCH_CLOSED" in e.value.text
+    bad_key = key.copy()
+    bad_key[0, 0, 6, 0] = np.uint64(q[6])
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.Switch(q, 14, dnum, key=bad_key)
+    assert "E_SWITCH_KEY_CANONICAL" in e.value.text

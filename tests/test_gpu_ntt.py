@@ -1,0 +1,156 @@
+"""GPU parity of the batched NTT/INTT against the oracle and the golden fixtures."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import closed_form as cf
+import oracle
+import praghip
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+C1 = cf.primes_below(54, 4096, 2)
+C2 = cf.primes_below(50, 16384, 6)
+
+
+def _roundtrip_case(q, log_n, limbs, seed, gpu, patterns=True):
+    n = 1 << log_n
+    print(f"[ntt] log_n={log_n} primes={len(q)} limbs={limbs} seed={seed:#x}", flush=True)
+    a = oracle.fill_residues(limbs, n, q, seed)
+    if patterns:  # check_resident.cpp:35 boundary pattern on the first limb
+        qq = np.uint64(q[0])
+        j = np.arange(n)
+        a[0, j % 13 == 0] = 0
+        a[0, j % 13 == 1] = qq - np.uint64(1)
+        a[0, j % 13 == 2] = 1
+    tab = oracle.Tables(q, log_n)
+    plan = praghip.NttBatch(q, log_n, device=0)
+    t = to_dev(a)
+    plan.forward(t)
+    got = from_dev(t)
+    want = oracle.ntt(a, tab)
+    np.testing.assert_array_equal(got, want)
+    plan.inverse(t)
+    np.testing.assert_array_equal(from_dev(t), a)
+    # inverse on arbitrary (non-transform) input against the oracle inverse
+    b = oracle.fill_residues(limbs, n, q, seed + 1)
+    tb = to_dev(b)
+    plan.inverse(tb)
+    np.testing.assert_array_equal(from_dev(tb), oracle.ntt(b, tab, inverse=True))
+
+
+def test_ntt_locked_primes(gpu):
+    _roundtrip_case(cf.LOCKED_PRIMES, 14, 14, 0x5052414700000101, gpu)
+
+
+def test_ntt_c2_primes_f64_path(gpu):
+    _roundtrip_case(C2, 14, 24, 0x5052414700000102, gpu)
+
+
+def test_ntt_c1_config(gpu):
+    # C1: N=4096, 2 primes ~54 bits, 16 polynomials x 2 limbs
+    _roundtrip_case(C1, 12, 32, 0x5052414700000001, gpu)
+
+
+@pytest.mark.parametrize("log_n", [4, 5, 6, 7, 9, 11, 13])
+def test_ntt_all_sizes(gpu, log_n):
+    n = 1 << log_n
+    q = [cf.primes_below(60, n, 1)[0], cf.primes_below(50, n, 1)[0], cf.primes_below(62, n, 1)[0]]
+    _roundtrip_case(q, log_n, 6, 0x77 + log_n, gpu, patterns=False)
+
+
+def test_ntt_golden_small(gpu, golden_dir):
+    data = np.load(os.path.join(golden_dir, "ntt_small.npz"))
+    names = sorted({k.rsplit("_", 1)[0] for k in data.files})
+    done = 0
+    for name in names:
+        a = data[name + "_in"]
+        if a.size < 16:
+            continue  # the GPU plans start at N=16
+        q = int(data[name + "_q"][0])
+        plan = praghip.NttBatch([q], a.size.bit_length() - 1)
+        t = to_dev(a[None])
+        plan.forward(t)
+        np.testing.assert_array_equal(from_dev(t)[0], data[name + "_out"], err_msg=name)
+        done += 1
+    assert done >= 8
+
+
+def test_ntt_golden_sampled_full_size(gpu, golden_dir):
+    with open(os.path.join(golden_dir, "ntt_sampled.json")) as f:
+        cases = json.load(f)
+    for case in cases:
+        q, log_n, seed = int(case["q"]), case["log_n"], int(case["seed"])
+        a = oracle.fill_residues(1, 1 << log_n, [q], seed)
+        plan = praghip.NttBatch([q], log_n)
+        t = to_dev(a)
+        plan.forward(t)
+        out = from_dev(t)[0]
+        for k, e in zip(case["k"], case["expected"]):
+            assert int(out[k]) == int(e), (case["set"], q, k)
+
+
+def test_ntt_c2_full_batch_properties(gpu):
+    """C2 at full size: 256 ciphertexts x 2 x 6 primes = 3072 limbs.  Bit-exact
+    forward against the oracle on a slice, round trip and linearity on all."""
+    import torch
+    n, limbs = 16384, 3072
+    q = C2
+    plan = praghip.NttBatch(q, 14)
+    a = oracle.fill_residues(limbs, n, q, 0x5052414700000002)
+    t = to_dev(a)
+    plan.forward(t)
+    fwd = from_dev(t)
+    tab = oracle.Tables(q, 14)
+    np.testing.assert_array_equal(fwd[:96], oracle.ntt(a[:96], tab))
+    np.testing.assert_array_equal(fwd[-60:], oracle.ntt(a[-60:], tab))
+    plan.inverse(t)
+    assert torch.equal(t, to_dev(a))
+    # linearity: NTT(a + b) = NTT(a) + NTT(b) mod q
+    b = oracle.fill_residues(limbs, n, q, 0x5052414700000003)
+    qcol = np.array([q[l % 6] for l in range(limbs)], dtype=np.uint64)[:, None]
+    s = (a + b) % qcol
+    ts, tb = to_dev(s), to_dev(b)
+    plan.forward(ts)
+    plan.forward(tb)
+    np.testing.assert_array_equal(from_dev(ts), (fwd + from_dev(tb)) % qcol)
+
+
+def test_ntt_host_api_and_errors(gpu):
+    q = cf.LOCKED_PRIMES[:6]
+    plan = praghip.NttBatch(q, 14, batches=2)
+    a = oracle.fill_residues(12, 16384, q, 99)
+    out = plan.transform(a)
+    np.testing.assert_array_equal(out, oracle.ntt(a, oracle.Tables(q, 14)))
+    np.testing.assert_array_equal(plan.transform(out, inverse=True), a)
+    bad = a.copy()
+    bad[3, 7] = np.uint64(q[3])
+    with pytest.raises(praghip.PraghipError) as e:
+        plan.transform(bad)
+    assert "E_NTT_CANONICAL_REQUIRED" in e.value.text
+    with pytest.raises(praghip.PraghipError):
+        plan.transform(a[:6])
+    # client phase: NTT -> (.) key -> INTT (ntt.cu:181-199) = negacyclic product with the key
+    key = oracle.fill_residues(6, 16384, q, 5)
+    plan.bind_client_key(key)
+    got = plan.client_phase(a)
+    tab = oracle.Tables(q, 14)
+    prod = np.empty_like(a)
+    fa = oracle.ntt(a, tab)
+    for l in range(12):
+        qq = q[l % 6]
+        prod[l] = [(int(x) * int(y)) % qq for x, y in zip(fa[l], key[l % 6])]
+    np.testing.assert_array_equal(got, oracle.ntt(prod, tab, inverse=True))
+    t = plan.timing()
+    assert t.kernel_ms > 0 and t.sensitive_bytes == 12 * 16384 * 8 + 6 * 16384 * 16
+    c = plan.close()
+    assert c.closed and c.first_hip_error == 0
+    assert c.wipe_synchronized_bytes == c.freed_bytes == t.sensitive_bytes
+    c2 = plan.close()
+    assert c2.freed_bytes == t.sensitive_bytes  # idempotent
+    with pytest.raises(praghip.PraghipError) as e:
+        plan.transform(a)
+    assert "E_NTT_CLOSED" in e.value.text
