@@ -140,6 +140,17 @@ def bench_gemm(torch, praghip, steps, warmup):
     }
 
 
+def bench_copy(torch, steps, warmup):
+    """Plain device copy of 384 MiB (the bytes one NTT launch reads, and again writes):
+    the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
+    src = torch.empty(3072 * N, dtype=torch.int64, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    ms = Timer(torch).run(lambda: dst.copy_(src), steps, warmup)
+    nbytes = src.numel() * 8
+    return {"bytes_each_way": nbytes, "ms_per_step": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
 def cpu_baselines(torch, res, budget_s: float):
     """Oracle timings on bounded samples (rank 0, N=1 only)."""
     import numpy as np
@@ -198,7 +209,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm"], default="all")
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
     args = ap.parse_args()
@@ -211,6 +222,13 @@ def main() -> int:
     import praghip
     assert torch.cuda.is_available() and praghip.device_count() >= 1, "needs an MI355X"
     res = {}
+    if args.only == "copy":
+        r = bench_copy(torch, args.steps, args.warmup)
+        log(f"copy {r['bytes_each_way']} B each way: {r['gbs']:.1f} GB/s")
+        print(json.dumps({"metric": "device copy (calibration)", "value": r["gbs"], "unit": "GB/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+                          "higher_is_better": True, "bytes_each_way": r["bytes_each_way"]}), flush=True)
+        return 0
     if args.only in ("all", "ntt"):
         log("NTT C2 ...")
         res["ntt"] = bench_ntt(torch, praghip, args.steps, args.warmup)

@@ -222,7 +222,7 @@ void release_all(int device, Buffers& buf, hipStream_t& stream, hipEvent_t* even
 struct NttHost {
   std::vector<NttPrime> primes;
   std::vector<ulonglong2> fwd_u, inv_u;
-  std::vector<double2> fwd_f, inv_f;
+  std::vector<double> fwd_f, inv_f;
 };
 
 // Builds the per-prime constants and device-format tables of a prime set.
@@ -261,14 +261,12 @@ int build_ntt_host(const uint64_t* q, size_t P, unsigned log_n, const uint64_t* 
     pr.qd = double(qq);
     pr.qinv = 1.0 / double(qq);
     pr.ninv_f = double(invn[0]);
-    pr.ninv_fq = double(invn[0]) / double(qq);
     pr.last_f = double(last);
-    pr.last_fq = double(last) / double(qq);
     for (size_t i = 0; i < n; ++i) {
       h.fwd_u[p * n + i] = make_ulonglong2(fwd[2 * i], fwd[2 * i + 1]);
       h.inv_u[p * n + i] = make_ulonglong2(inv[2 * i], inv[2 * i + 1]);
-      h.fwd_f[p * n + i] = make_double2(double(fwd[2 * i]), double(fwd[2 * i]) / double(qq));
-      h.inv_f[p * n + i] = make_double2(double(inv[2 * i]), double(inv[2 * i]) / double(qq));
+      h.fwd_f[p * n + i] = double(fwd[2 * i]);
+      h.inv_f[p * n + i] = double(inv[2 * i]);
     }
   }
   return PRAGHIP_OK;
@@ -282,13 +280,23 @@ hipError_t upload_ntt(const NttHost& h, unsigned log_n, Buffers& buf, NttDevice&
   if ((e = buf.alloc((void**)&d.primes, P * sizeof(NttPrime), false)) != hipSuccess) return e;
   if ((e = buf.alloc((void**)&d.tw_fwd_u, P * n * 16, false)) != hipSuccess) return e;
   if ((e = buf.alloc((void**)&d.tw_inv_u, P * n * 16, false)) != hipSuccess) return e;
-  if ((e = buf.alloc((void**)&d.tw_fwd_f, P * n * 16, false)) != hipSuccess) return e;
-  if ((e = buf.alloc((void**)&d.tw_inv_f, P * n * 16, false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.tw_fwd_f, P * n * 8, false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.tw_inv_f, P * n * 8, false)) != hipSuccess) return e;
+  for (size_t p = 0; p < P; ++p) {
+    if (h.primes[p].use_f64)
+      d.host_sel_f64[d.n_f64++] = int(p);
+    else
+      d.host_sel_u64[d.n_u64++] = int(p);
+  }
+  if ((e = buf.alloc((void**)&d.sel_f64, 64 * sizeof(int), false)) != hipSuccess) return e;
+  if ((e = buf.alloc((void**)&d.sel_u64, 64 * sizeof(int), false)) != hipSuccess) return e;
+  if ((e = hipMemcpyAsync(d.sel_f64, d.host_sel_f64, 64 * sizeof(int), hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.sel_u64, d.host_sel_u64, 64 * sizeof(int), hipMemcpyHostToDevice, s))) return e;
   if ((e = hipMemcpyAsync(d.primes, h.primes.data(), P * sizeof(NttPrime), hipMemcpyHostToDevice, s))) return e;
   if ((e = hipMemcpyAsync(d.tw_fwd_u, h.fwd_u.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
   if ((e = hipMemcpyAsync(d.tw_inv_u, h.inv_u.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
-  if ((e = hipMemcpyAsync(d.tw_fwd_f, h.fwd_f.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
-  if ((e = hipMemcpyAsync(d.tw_inv_f, h.inv_f.data(), P * n * 16, hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.tw_fwd_f, h.fwd_f.data(), P * n * 8, hipMemcpyHostToDevice, s))) return e;
+  if ((e = hipMemcpyAsync(d.tw_inv_f, h.inv_f.data(), P * n * 8, hipMemcpyHostToDevice, s))) return e;
   return hipStreamSynchronize(s);
 }
 

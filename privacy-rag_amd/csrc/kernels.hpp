@@ -16,8 +16,13 @@ struct NttDevice {
   NttPrime* primes = nullptr;        // [P]
   ulonglong2* tw_fwd_u = nullptr;    // [P][N] (w, floor(w 2^64/q))
   ulonglong2* tw_inv_u = nullptr;    // [P][N]
-  double2* tw_fwd_f = nullptr;       // [P][N] (w, w/q) for q < 2^50
-  double2* tw_inv_f = nullptr;       // [P][N]
+  double* tw_fwd_f = nullptr;        // [P][N] w as a double, for q < 2^50
+  double* tw_inv_f = nullptr;        // [P][N]
+  // prime indices handled by the float path (q < 2^50) and by the integer path
+  int* sel_f64 = nullptr;            // device [n_f64]
+  int* sel_u64 = nullptr;            // device [n_u64]
+  int n_f64 = 0, n_u64 = 0;
+  int host_sel_f64[64] = {}, host_sel_u64[64] = {};
 };
 
 hipError_t launch_ntt(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d, hipStream_t s);

@@ -10,59 +10,118 @@
 
 namespace praghip {
 
-template <int LOGN, bool INV, class A>
-__device__ __forceinline__ void ntt_limb(uint64_t* __restrict__ x, const typename A::TW* __restrict__ tw,
-                                         const NttPrime& pr, typename A::T* lds) {
-  using T = typename A::T;
-  const unsigned t = threadIdx.x;
-  const A ar(pr);
-  T v[16];
+// Raw loads of one limb in the layout the first pass of the transform uses:
+// forward - coalesced across threads; inverse - runs of 2^RSHORT consecutive
+// coefficients per (thread, block), read as 16-byte pairs.
+template <int LOGN, bool INV>
+__device__ __forceinline__ void load_limb(uint64_t (&r)[kE], const uint64_t* __restrict__ x, unsigned t) {
   if (!INV) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = ar.from_u64(x[fwd_in_index<LOGN>(t, j)]);
-    ntt_fwd_regs<LOGN>(v, lds, t, tw, ar);
-    ulonglong2* out = reinterpret_cast<ulonglong2*>(x + (size_t(t) << 4));
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) out[j / 2] = make_ulonglong2(ar.to_u64_fwd(v[j]), ar.to_u64_fwd(v[j + 1]));
+    for (int j = 0; j < kE; ++j) r[j] = x[fwd_in_index<LOGN>(t, j)];
   } else {
-    const ulonglong2* in = reinterpret_cast<const ulonglong2*>(x + (size_t(t) << 4));
 #pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      const ulonglong2 p = in[j / 2];
-      v[j] = ar.from_u64(p.x);
-      v[j + 1] = ar.from_u64(p.y);
+    for (int j = 0; j < kE; j += 2) {
+      const ulonglong2 p = *reinterpret_cast<const ulonglong2*>(x + inv_in_index<LOGN>(t, j));
+      r[j] = p.x;
+      r[j + 1] = p.y;
     }
-    ntt_inv_regs<LOGN>(v, lds, t, tw, ar, pr);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) x[inv_out_index<LOGN>(t, j)] = ar.to_u64_inv(v[j]);
   }
 }
 
-template <int LOGN, bool INV>
-__global__ void __launch_bounds__((1 << LOGN) / 16)
-    ntt_kernel(uint64_t* __restrict__ data, const NttPrime* __restrict__ primes,
-               const ulonglong2* __restrict__ tw_u, const double2* __restrict__ tw_f, int P) {
+// Transform of one limb: load, transform in registers + LDS, store.
+template <int LOGN, bool INV, class A>
+__device__ __forceinline__ void transform_limb(uint64_t* __restrict__ x, const typename A::TW* __restrict__ tab,
+                                               const NttPrime& pr, typename A::T* lds) {
+  using T = typename A::T;
+  const unsigned t = threadIdx.x;
+  const A ar(pr);
+  uint64_t r[kE];
+  load_limb<LOGN, INV>(r, x, t);
+  T v[kE];
+#pragma unroll
+  for (int j = 0; j < kE; ++j) v[j] = ar.from_u64(r[j]);
+  ntt_regs<LOGN, INV>(v, lds, t, tab, ar, pr);
+  if (!INV) {
+#pragma unroll
+    for (int j = 0; j < kE; j += 2)
+      *reinterpret_cast<ulonglong2*>(x + fwd_out_index<LOGN>(t, j)) =
+          make_ulonglong2(ar.to_u64_fwd(v[j]), ar.to_u64_fwd(v[j + 1]));
+  } else {
+#pragma unroll
+    for (int j = 0; j < kE; ++j) x[inv_out_index<LOGN>(t, j)] = ar.to_u64_inv(v[j]);
+  }
+}
+
+// Kernel over the limbs whose prime uses arithmetic A: virtual index v maps to
+// limb (v / C) * P + sel[v % C], where sel lists the C prime indices of that
+// arithmetic.  Workgroup g transforms v = g, g + G, ... (G resident
+// workgroups).
+template <int LOGN, bool INV, class A>
+__global__ void __launch_bounds__(ntt_threads<LOGN>())
+    ntt_kernel(uint64_t* __restrict__ data, size_t count, const NttPrime* __restrict__ primes,
+               const typename A::TW* __restrict__ tw, int P, const int* __restrict__ sel, int C) {
   __shared__ uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
-  const size_t limb = blockIdx.x;
-  const int p = int(limb % unsigned(P));
-  const NttPrime pr = primes[p];
-  uint64_t* x = data + (limb << LOGN);
-  const size_t toff = size_t(p) << LOGN;
-  if (pr.use_f64)
-    ntt_limb<LOGN, INV, ArF64>(x, tw_f + toff, pr, reinterpret_cast<double*>(lds));
-  else
-    ntt_limb<LOGN, INV, ArU64>(x, tw_u + toff, pr, lds);
+  for (size_t v = blockIdx.x; v < count; v += gridDim.x) {
+    const size_t limb = (v / unsigned(C)) * unsigned(P) + unsigned(sel[v % unsigned(C)]);
+    const int p = int(limb % unsigned(P));
+    const NttPrime pr = primes[p];
+    transform_limb<LOGN, INV, A>(data + (limb << LOGN), tw + (size_t(p) << LOGN), pr,
+                                 reinterpret_cast<typename A::T*>(lds));
+  }
+}
+
+// Resident workgroups per CU times the CU count, cached per kernel.
+template <int LOGN, bool INV, class A>
+static unsigned persistent_grid() {
+  static unsigned grid = 0;
+  if (!grid) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ntt_kernel<LOGN, INV, A>, ntt_threads<LOGN>(), 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    grid = unsigned(cus * per_cu);
+  }
+  return grid;
+}
+
+// Number of limbs among the first `limbs` whose prime index is in sel[0..C).
+static size_t subset_count(size_t limbs, int P, const int* host_sel, int C) {
+  size_t count = (limbs / unsigned(P)) * unsigned(C);
+  const size_t tail = limbs % unsigned(P);
+  for (int c = 0; c < C; ++c) count += size_t(host_sel[c]) < tail ? 1 : 0;
+  return count;
+}
+
+template <int LOGN, bool INV, class A>
+static hipError_t launch_subset(uint64_t* data, size_t limbs, const NttDevice& d, const typename A::TW* tw,
+                                const int* sel_dev, const int* sel_host, int C, hipStream_t s) {
+  if (!C) return hipSuccess;
+  const size_t count = subset_count(limbs, d.P, sel_host, C);
+  if (!count) return hipSuccess;
+  const dim3 block{unsigned(ntt_threads<LOGN>())};
+  const dim3 grid{unsigned(std::min<size_t>(count, persistent_grid<LOGN, INV, A>()))};
+  hipLaunchKernelGGL((ntt_kernel<LOGN, INV, A>), grid, block, 0, s, data, count, d.primes, tw, d.P, sel_dev, C);
+  return hipGetLastError();
 }
 
 template <int LOGN>
 static hipError_t launch_ntt_n(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d,
                                hipStream_t s) {
-  const dim3 grid{unsigned(limbs)}, block{unsigned((1 << LOGN) / 16)};
-  if (inverse)
-    hipLaunchKernelGGL((ntt_kernel<LOGN, true>), grid, block, 0, s, data, d.primes, d.tw_inv_u, d.tw_inv_f, d.P);
-  else
-    hipLaunchKernelGGL((ntt_kernel<LOGN, false>), grid, block, 0, s, data, d.primes, d.tw_fwd_u, d.tw_fwd_f, d.P);
-  return hipGetLastError();
+  hipError_t e;
+  if (inverse) {
+    e = launch_subset<LOGN, true, ArF64>(data, limbs, d, d.tw_inv_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
+    if (e == hipSuccess)
+      e = launch_subset<LOGN, true, ArU64>(data, limbs, d, d.tw_inv_u, d.sel_u64, d.host_sel_u64, d.n_u64, s);
+  } else {
+    e = launch_subset<LOGN, false, ArF64>(data, limbs, d, d.tw_fwd_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
+    if (e == hipSuccess)
+      e = launch_subset<LOGN, false, ArU64>(data, limbs, d, d.tw_fwd_u, d.sel_u64, d.host_sel_u64, d.n_u64, s);
+  }
+  return e;
 }
 
 hipError_t launch_ntt(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d, hipStream_t s) {

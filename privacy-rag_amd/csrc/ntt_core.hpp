@@ -5,17 +5,23 @@
 // stage() ntt.cu:42-53): forward stage s has gap N>>(s+1) and twiddle
 // fwd[(1<<s) + group]; inverse stage l has gap 1<<l and twiddle
 // inv[N-(N>>l)+1+group], and the last inverse stage scales by N^-1.  Those
-// stages are grouped four at a time into radix-16 register passes: a pass
-// over the gap bits [LO, LO+R) gives each thread the 2^R coefficients that
-// differ only in those bits.  Between passes the limb is exchanged through LDS
-// (one 8-byte slot per coefficient plus one pad slot per 16, which keeps every
+// stages are grouped four at a time into radix-16 register passes: a pass over
+// the gap bits [LO, LO+R) gives each thread the 2^R coefficients that differ
+// only in those bits.  Between passes the limb is exchanged through LDS (one
+// 8-byte slot per coefficient plus one pad slot per 16, which keeps every
 // pass's access pattern free of bank conflicts).
+//
+// Twiddles: a pass's twiddles are loaded into registers in one batch - for the
+// float path while the previous pass computes, so their L2 latency hides
+// behind a whole pass of arithmetic; for the integer path (16-byte pairs, too
+// many registers to hold two passes) at the start of the pass, one wait per
+// pass.
 //
 // Arithmetic policies:
 //   ArU64 - any q < 2^62: Harvey's lazy butterflies (forward values in [0,4q),
-//           inverse in [0,2q)) over Shoup twiddles, canonicalised at the end;
-//   ArF64 - q < 2^50: residues as exact doubles, FMA-based products, centred
-//           values re-centred every second stage.
+//           inverse in [0,2q)) over Shoup twiddle pairs, canonical at the end;
+//   ArF64 - q < 2^50: residues as exact integers in doubles, products with an
+//           error-free FMA split, centred values re-centred every second stage.
 // Both produce the canonical residue of the same transform, so the result is
 // bit-identical to the reference whatever the path.
 #pragma once
@@ -29,25 +35,25 @@ struct NttPrime {
   uint64_t ninv, ninv_q;      // N^-1 mod q (Shoup pair)
   uint64_t last, last_q;      // w_last * N^-1 (Shoup pair), w_last = inv[N-1]
   double qd, qinv;            // q and 1/q as doubles (float path)
-  double ninv_f, ninv_fq;     // N^-1 as (w, w/q)
-  double last_f, last_fq;     // w_last * N^-1 as (w, w/q)
+  double ninv_f, last_f;      // N^-1 and w_last * N^-1 as doubles
   int use_f64;                // q < 2^50: the float path is exact
   int pad;
 };
 
 __device__ __forceinline__ unsigned lds_pos(unsigned x) { return x + (x >> 4); }
 
+constexpr int kLogE = 4;  // 16 coefficients per thread
+constexpr int kE = 1 << kLogE;
+
 // Index of the j-th register coefficient of thread t in a pass over the gap
 // bits [LO, LO+R).  When R < 4 each thread runs 16>>R independent radix-2^R
-// blocks; SUB_MINOR puts the block number in the low bits of the thread's
-// identity (16 consecutive coefficients per thread), otherwise in the high bits
-// (consecutive threads on consecutive coefficients).
-template <int LOGN, int LO, int R, bool SUB_MINOR>
+// blocks; block b acts as thread t + b*THREADS, so consecutive threads stay on
+// consecutive coefficients whenever LO > 0.
+template <int LOGN, int LO, int R>
 __device__ __forceinline__ unsigned elem_index(unsigned t, int j) {
-  constexpr int SUB = 16 >> R;
-  constexpr unsigned THREADS = (1u << LOGN) / 16;
+  constexpr unsigned THREADS = (1u << LOGN) >> kLogE;
   const int b = j >> R, jl = j & ((1 << R) - 1);
-  const unsigned T = SUB_MINOR ? (t * SUB + b) : (t + unsigned(b) * THREADS);
+  const unsigned T = t + unsigned(b) * THREADS;
   const unsigned lo = T & ((1u << LO) - 1), hi = T >> LO;
   return (hi << (LO + R)) | (unsigned(jl) << LO) | lo;
 }
@@ -55,7 +61,8 @@ __device__ __forceinline__ unsigned elem_index(unsigned t, int j) {
 // ---------------------------------------------------------------- policies
 struct ArU64 {
   using T = uint64_t;
-  using TW = ulonglong2;
+  using TW = ulonglong2;  // (w, floor(w 2^64 / q))
+  static constexpr bool kAhead = false;  // 16-byte twiddles: load at the pass start
   uint64_t q, q2;
   __device__ explicit ArU64(const NttPrime& p) : q(p.q), q2(p.q2) {}
   __device__ __forceinline__ T from_u64(uint64_t x) const { return x; }
@@ -85,9 +92,18 @@ struct ArU64 {
   __device__ __forceinline__ void settle(T&) const {}
 };
 
+// Float path bounds (q < 2^50, so q * 2^-52 < 1/4).  For |a| <= B q the
+// quotient estimate c = rint(a * fl(w * fl(1/q))) is within 1/2 + B/4 of
+// a w / q, so |a w - c q| <= (1/2 + B/4) q, computed exactly (an integer
+// below 2^53 formed by FMAs from the error-free split of a w).
+//   forward : every value re-centred to <= q/2 + 1 each second stage; in
+//             between B <= 1.13 and outputs stay below 2.7 q;
+//   inverse : sums re-centred every stage, differences go through the
+//             product, so every value stays <= q.
 struct ArF64 {
   using T = double;
-  using TW = double2;
+  using TW = double;  // w; w/q is formed in registers
+  static constexpr bool kAhead = true;  // load the next pass's twiddles one pass early
   double q, qinv;
   __device__ explicit ArF64(const NttPrime& p) : q(p.qd), qinv(p.qinv) {}
   __device__ __forceinline__ T from_u64(uint64_t x) const { return (double)x; }
@@ -98,8 +114,9 @@ struct ArF64 {
   }
   __device__ __forceinline__ uint64_t to_u64_fwd(T x) const { return to_u64(x); }
   __device__ __forceinline__ uint64_t to_u64_inv(T x) const { return to_u64(x); }
+  __device__ __forceinline__ T mul(T a, TW w) const { return mul_f64(a, w, w * qinv, q); }
   __device__ __forceinline__ void fwd(T& x, T& y, TW w) const {
-    const T t = mul_f64(y, w.x, w.y, q);
+    const T t = mul(y, w);
     const T a = x;
     x = a + t;
     y = a - t;
@@ -107,38 +124,70 @@ struct ArF64 {
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
     const T s = x + y, d = x - y;
     x = reduce_f64(s, q, qinv);
-    y = mul_f64(d, w.x, w.y, q);
+    y = mul(d, w);
   }
   __device__ __forceinline__ void inv_last(T& x, T& y, const NttPrime& p) const {
     const T s = x + y, d = x - y;
-    x = mul_f64(s, p.ninv_f, p.ninv_fq, q);
-    y = mul_f64(d, p.last_f, p.last_fq, q);
+    x = mul(s, p.ninv_f);
+    y = mul(d, p.last_f);
   }
   __device__ __forceinline__ void settle(T& x) const { x = reduce_f64(x, q, qinv); }
 };
 
 // ------------------------------------------------------------------ passes
-// Forward radix-2^R pass over gap bits [LO, LO+R): global stages
-// s = LOGN-LO-R .. LOGN-LO-1.
-template <int LOGN, int LO, int R, bool SUB_MINOR, class A>
-__device__ __forceinline__ void fwd_pass(typename A::T (&v)[16], unsigned t,
-                                         const typename A::TW* __restrict__ tw, const A& ar) {
-  constexpr int SUB = 16 >> R;
-  constexpr unsigned THREADS = (1u << LOGN) / 16;
+// Twiddles of one pass: SUB blocks x (2^R - 1) entries, in the order the pass
+// consumes them (block, stage, group).
+template <int R>
+constexpr int pass_twiddles() { return (kE >> R) * ((1 << R) - 1); }
+
+template <int LOGN, int LO, int R, bool INV, class TW>
+__device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<R>()], unsigned t,
+                                                   const TW* __restrict__ tab) {
+  constexpr int SUB = kE >> R;
+  constexpr unsigned N = 1u << LOGN, THREADS = N >> kLogE;
+  int n = 0;
 #pragma unroll
   for (int b = 0; b < SUB; ++b) {
-    const unsigned T = SUB_MINOR ? (t * SUB + b) : (t + unsigned(b) * THREADS);
-    const unsigned hi = T >> LO;
+    // With LO >= 6 all 64 lanes of a wave share hi: the twiddle addresses are
+    // wave-uniform and the loads go through the scalar unit into SGPRs.
+    const unsigned hi_lane = (t + unsigned(b) * THREADS) >> LO;
+    const unsigned hi = LO >= 6 ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (!INV) {
+        const int s = LOGN - LO - R + i;
+#pragma unroll
+        for (int k = 0; k < (1 << i); ++k) w[n++] = tab[(1u << s) + (hi << i) + k];
+      } else {
+        const int l = LO + i;
+#pragma unroll
+        for (int k = 0; k < (1 << (R - 1 - i)); ++k) {
+          if (l != LOGN - 1) w[n] = tab[N - (N >> l) + 1 + (hi << (R - 1 - i)) + k];
+          ++n;
+        }
+      }
+    }
+  }
+}
+
+// Forward radix-2^R pass over gap bits [LO, LO+R): global stages
+// s = LOGN-LO-R .. LOGN-LO-1.
+template <int LOGN, int LO, int R, class A>
+__device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename A::TW (&w)[pass_twiddles<R>()],
+                                         const A& ar) {
+  constexpr int SUB = kE >> R;
+  int n = 0;
+#pragma unroll
+  for (int b = 0; b < SUB; ++b) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int s = LOGN - LO - R + i, g = R - 1 - i;
 #pragma unroll
-      for (int k = 0; k < (1 << i); ++k) {
-        const typename A::TW w = tw[(1u << s) + (hi << i) + k];
+      for (int k = 0; k < (1 << i); ++k, ++n) {
 #pragma unroll
         for (int m = 0; m < (1 << g); ++m) {
           const int j0 = (b << R) | (k << (g + 1)) | m, j1 = j0 | (1 << g);
-          ar.fwd(v[j0], v[j1], w);
+          ar.fwd(v[j0], v[j1], w[n]);
         }
       }
       if (s & 1) {
@@ -150,126 +199,122 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[16], unsigned t,
 }
 
 // Inverse radix-2^R pass over gap bits [LO, LO+R): stages l = LO .. LO+R-1.
-template <int LOGN, int LO, int R, bool SUB_MINOR, class A>
-__device__ __forceinline__ void inv_pass(typename A::T (&v)[16], unsigned t,
-                                         const typename A::TW* __restrict__ tw, const A& ar,
-                                         const NttPrime& pr) {
-  constexpr int SUB = 16 >> R;
-  constexpr unsigned N = 1u << LOGN, THREADS = N / 16;
+template <int LOGN, int LO, int R, class A>
+__device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename A::TW (&w)[pass_twiddles<R>()],
+                                         const A& ar, const NttPrime& pr) {
+  constexpr int SUB = kE >> R;
+  int n = 0;
 #pragma unroll
   for (int b = 0; b < SUB; ++b) {
-    const unsigned T = SUB_MINOR ? (t * SUB + b) : (t + unsigned(b) * THREADS);
-    const unsigned hi = T >> LO;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int l = LO + i;
-      if (l == LOGN - 1) {  // last stage: one group, twiddle and N^-1 folded
+#pragma unroll
+      for (int k = 0; k < (1 << (R - 1 - i)); ++k, ++n) {
 #pragma unroll
         for (int m = 0; m < (1 << i); ++m) {
-          const int j0 = (b << R) | m, j1 = j0 | (1 << i);
-          ar.inv_last(v[j0], v[j1], pr);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < (1 << (R - 1 - i)); ++k) {
-          const unsigned group = (hi << (R - 1 - i)) + k;
-          const typename A::TW w = tw[N - (N >> l) + 1 + group];
-#pragma unroll
-          for (int m = 0; m < (1 << i); ++m) {
-            const int j0 = (b << R) | (k << (i + 1)) | m, j1 = j0 | (1 << i);
-            ar.inv(v[j0], v[j1], w);
-          }
+          const int j0 = (b << R) | (k << (i + 1)) | m, j1 = j0 | (1 << i);
+          if (l == LOGN - 1)  // last stage: one group, twiddle and N^-1 folded
+            ar.inv_last(v[j0], v[j1], pr);
+          else
+            ar.inv(v[j0], v[j1], w[n]);
         }
       }
     }
   }
 }
 
-template <int LOGN, int LO0, int R0, bool SM0, int LO1, int R1, bool SM1, class T>
-__device__ __forceinline__ void exchange(T (&v)[16], T* lds, unsigned t) {
-#pragma unroll
-  for (int j = 0; j < 16; ++j) lds[lds_pos(elem_index<LOGN, LO0, R0, SM0>(t, j))] = v[j];
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = lds[lds_pos(elem_index<LOGN, LO1, R1, SM1>(t, j))];
-  __syncthreads();
-}
-
+// Pass geometry.  Forward passes take 4 gap bits from the top down, the last
+// one the remainder [0, RSHORT); inverse passes start with the remainder
+// [0, RSHORT) and continue upwards 4 bits at a time.  With that order the
+// forward input and inverse output are coalesced across threads, and the
+// forward output / inverse input come as 2^RSHORT consecutive coefficients per
+// (thread, block).
 template <int LOGN>
 struct Passes {
-  static constexpr int NP = (LOGN + 3) / 4;
-  static constexpr int RLAST = LOGN - 4 * (NP - 1);
-  // forward: high bits first; the last pass is [0, RLAST) with SUB_MINOR
-  static constexpr int fwd_lo(int p) { return p < NP - 1 ? LOGN - 4 * (p + 1) : 0; }
-  static constexpr int fwd_r(int p) { return p < NP - 1 ? 4 : RLAST; }
-  static constexpr bool fwd_sm(int p) { return p == NP - 1; }
-  // inverse: low bits first; the last pass is [LOGN-RLAST, LOGN) block-major
-  static constexpr int inv_lo(int p) { return 4 * p; }
-  static constexpr int inv_r(int p) { return p < NP - 1 ? 4 : RLAST; }
-  static constexpr bool inv_sm(int p) { return p == 0; }
+  static constexpr int NP = (LOGN + kLogE - 1) / kLogE;
+  static constexpr int RSHORT = LOGN - kLogE * (NP - 1);
+  static constexpr int fwd_lo(int p) { return p < NP - 1 ? LOGN - kLogE * (p + 1) : 0; }
+  static constexpr int fwd_r(int p) { return p < NP - 1 ? kLogE : RSHORT; }
+  static constexpr int inv_lo(int p) { return p == 0 ? 0 : RSHORT + kLogE * (p - 1); }
+  static constexpr int inv_r(int p) { return p == 0 ? RSHORT : kLogE; }
+  static constexpr int lo(bool inv, int p) { return inv ? inv_lo(p) : fwd_lo(p); }
+  static constexpr int r(bool inv, int p) { return inv ? inv_r(p) : fwd_r(p); }
 };
 
-template <int LOGN, int P, class A>
-__device__ __forceinline__ void fwd_from(typename A::T (&v)[16], typename A::T* lds, unsigned t,
-                                         const typename A::TW* tw, const A& ar) {
-  using S = Passes<LOGN>;
-  fwd_pass<LOGN, S::fwd_lo(P), S::fwd_r(P), S::fwd_sm(P)>(v, t, tw, ar);
-  if constexpr (P + 1 < S::NP) {
-    exchange<LOGN, S::fwd_lo(P), S::fwd_r(P), S::fwd_sm(P), S::fwd_lo(P + 1), S::fwd_r(P + 1),
-             S::fwd_sm(P + 1)>(v, lds, t);
-    fwd_from<LOGN, P + 1>(v, lds, t, tw, ar);
-  }
+template <int LOGN, int LO0, int R0, int LO1, int R1, class T>
+__device__ __forceinline__ void exchange(T (&v)[kE], T* lds, unsigned t) {
+#pragma unroll
+  for (int j = 0; j < kE; ++j) lds[lds_pos(elem_index<LOGN, LO0, R0>(t, j))] = v[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kE; ++j) v[j] = lds[lds_pos(elem_index<LOGN, LO1, R1>(t, j))];
+  __syncthreads();
 }
-template <int LOGN, int P, class A>
-__device__ __forceinline__ void inv_from(typename A::T (&v)[16], typename A::T* lds, unsigned t,
-                                         const typename A::TW* tw, const A& ar, const NttPrime& pr) {
+
+// Pass P with its twiddles already in registers; loads pass P+1's twiddles
+// first, then computes, exchanges and recurses.
+template <int LOGN, bool INV, int P, class A>
+__device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T* lds, unsigned t,
+                                           const typename A::TW* __restrict__ tab, const A& ar,
+                                           const NttPrime& pr,
+                                           const typename A::TW (&w)[pass_twiddles<Passes<LOGN>::r(INV, P)>()]) {
   using S = Passes<LOGN>;
-  inv_pass<LOGN, S::inv_lo(P), S::inv_r(P), S::inv_sm(P)>(v, t, tw, ar, pr);
+  constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
   if constexpr (P + 1 < S::NP) {
-    exchange<LOGN, S::inv_lo(P), S::inv_r(P), S::inv_sm(P), S::inv_lo(P + 1), S::inv_r(P + 1),
-             S::inv_sm(P + 1)>(v, lds, t);
-    inv_from<LOGN, P + 1>(v, lds, t, tw, ar, pr);
+    constexpr int LO1 = S::lo(INV, P + 1), R1 = S::r(INV, P + 1);
+    typename A::TW wn[pass_twiddles<R1>()];
+    if constexpr (A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
+    if constexpr (INV)
+      inv_pass<LOGN, LO, R>(v, w, ar, pr);
+    else
+      fwd_pass<LOGN, LO, R>(v, w, ar);
+    exchange<LOGN, LO, R, LO1, R1>(v, lds, t);
+    if constexpr (!A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
+    run_passes<LOGN, INV, P + 1>(v, lds, t, tab, ar, pr, wn);
+  } else {
+    if constexpr (INV)
+      inv_pass<LOGN, LO, R>(v, w, ar, pr);
+    else
+      fwd_pass<LOGN, LO, R>(v, w, ar);
   }
 }
 
-// Register layouts at the boundaries of a transform:
-//   forward input  : element (j << (LOGN-4)) | t   (coalesced across threads)
-//   forward output : element (t << 4) | j          (16 consecutive per thread)
-//   inverse input  : element (t << 4) | j
-//   inverse output : block-major last pass (coalesced across threads)
+// Whole-limb transform on register data (v holds the input layout on entry
+// and the output layout on exit; values stay in the policy's lazy form).
+template <int LOGN, bool INV, class A>
+__device__ __forceinline__ void ntt_regs(typename A::T (&v)[kE], typename A::T* lds, unsigned t,
+                                         const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr) {
+  using S = Passes<LOGN>;
+  typename A::TW w0[pass_twiddles<S::r(INV, 0)>()];
+  load_pass_twiddles<LOGN, S::lo(INV, 0), S::r(INV, 0), INV>(w0, t, tab);
+  run_passes<LOGN, INV, 0>(v, lds, t, tab, ar, pr, w0);
+}
+
+// Register layouts at the boundaries of a transform.
 template <int LOGN>
 __device__ __forceinline__ unsigned fwd_in_index(unsigned t, int j) {
   using S = Passes<LOGN>;
-  return elem_index<LOGN, S::fwd_lo(0), S::fwd_r(0), S::fwd_sm(0)>(t, j);
+  return elem_index<LOGN, S::fwd_lo(0), S::fwd_r(0)>(t, j);
 }
 template <int LOGN>
 __device__ __forceinline__ unsigned fwd_out_index(unsigned t, int j) {
   using S = Passes<LOGN>;
-  return elem_index<LOGN, S::fwd_lo(S::NP - 1), S::fwd_r(S::NP - 1), S::fwd_sm(S::NP - 1)>(t, j);
+  return elem_index<LOGN, S::fwd_lo(S::NP - 1), S::fwd_r(S::NP - 1)>(t, j);
 }
 template <int LOGN>
 __device__ __forceinline__ unsigned inv_in_index(unsigned t, int j) {
   using S = Passes<LOGN>;
-  return elem_index<LOGN, S::inv_lo(0), S::inv_r(0), S::inv_sm(0)>(t, j);
+  return elem_index<LOGN, S::inv_lo(0), S::inv_r(0)>(t, j);
 }
 template <int LOGN>
 __device__ __forceinline__ unsigned inv_out_index(unsigned t, int j) {
   using S = Passes<LOGN>;
-  return elem_index<LOGN, S::inv_lo(S::NP - 1), S::inv_r(S::NP - 1), S::inv_sm(S::NP - 1)>(t, j);
+  return elem_index<LOGN, S::inv_lo(S::NP - 1), S::inv_r(S::NP - 1)>(t, j);
 }
 
-// Whole-limb transforms on register data (v holds the input layout on entry
-// and the output layout on exit; values stay in the policy's lazy form).
-template <int LOGN, class A>
-__device__ __forceinline__ void ntt_fwd_regs(typename A::T (&v)[16], typename A::T* lds, unsigned t,
-                                             const typename A::TW* tw, const A& ar) {
-  fwd_from<LOGN, 0>(v, lds, t, tw, ar);
-}
-template <int LOGN, class A>
-__device__ __forceinline__ void ntt_inv_regs(typename A::T (&v)[16], typename A::T* lds, unsigned t,
-                                             const typename A::TW* tw, const A& ar, const NttPrime& pr) {
-  inv_from<LOGN, 0>(v, lds, t, tw, ar, pr);
-}
+template <int LOGN>
+constexpr int ntt_threads() { return (1 << LOGN) >> kLogE; }
 
 constexpr size_t lds_bytes(int log_n) { return (((size_t)1 << log_n) + ((size_t)1 << log_n) / 16) * 8; }
 
