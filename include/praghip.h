@@ -82,7 +82,8 @@ int praghip_ntt_plan_create(int device, const uint64_t *q, size_t primes, uint32
                             const uint64_t *invn_pairs, size_t batches, praghip_ntt_plan **plan);
 /* In-place batched transforms over device [limbs][N], limb l on prime l % primes
  * (ntt.cu:104-127 stage loop).  forward: natural -> bit-reversed order;
- * inverse: bit-reversed -> natural.  Inputs must be canonical. */
+ * inverse: bit-reversed -> natural.  Inputs must be canonical; data must be
+ * 16-byte aligned. */
 int praghip_ntt_forward(praghip_ntt_plan *plan, uint64_t *data, size_t limbs, void *stream);
 int praghip_ntt_inverse(praghip_ntt_plan *plan, uint64_t *data, size_t limbs, void *stream);
 /* NttBatch::transform (ntt.cu:145-168): host [batches][primes][N] in and out,

@@ -13,7 +13,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/praghip.h"
+#include "praghip.h"
 #include "kernels.hpp"
 
 namespace praghip {
@@ -403,6 +403,7 @@ static int ntt_device(praghip_ntt_plan* p, uint64_t* data, size_t limbs, void* s
   if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_NTT_CLOSED");
   if (!data && limbs) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (reinterpret_cast<uintptr_t>(data) & 15) return fail(PRAGHIP_E_ARGUMENT, "E_NTT_ALIGNMENT: 16-byte aligned data");
   if (limbs > (1ull << 31)) return fail(PRAGHIP_E_SHAPE, "E_NTT_SHAPE");
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
@@ -670,6 +671,9 @@ int praghip_keyswitch(praghip_switch_plan* p, const uint64_t* input, uint64_t* o
   if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
   if (batch && (!input || !output)) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (input == output && batch) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ALIAS");
+  if ((reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(output) |
+       reinterpret_cast<uintptr_t>(keys)) & 7)
+    return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ALIGNMENT: 8-byte aligned buffers");
   if (!keys && !p->key) return fail(PRAGHIP_E_STATE, "E_SWITCH_NO_KEY");
   uint32_t ginv = 1;
   if (!galois_inverse(galois_elt, p->log_n, ginv)) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ELEMENT");
@@ -749,6 +753,9 @@ int praghip_share_gemm(int device, const uint64_t* x, const void* w, int w_bits,
   if (w_bits != 8 && w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
   if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
   if (k >= (1u << 17) || m >= (1u << 31) || n >= (1u << 31)) return fail(PRAGHIP_E_SHAPE, "E_SHARE_SHAPE");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7 ||
+      (w_bits == 32 && (reinterpret_cast<uintptr_t>(w) & 3)))
+    return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
   DeviceScope scope(device);
   hipError_t e = scope.status();
   if (e == hipSuccess)

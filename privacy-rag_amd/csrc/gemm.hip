@@ -59,7 +59,8 @@ __device__ __forceinline__ int weight_digit(int w, int e) {
 template <int WB>
 __global__ void __launch_bounds__(kThreads)
     share_gemm_kernel(const uint64_t* __restrict__ x, const void* __restrict__ wv, const int8_t* __restrict__ shifts,
-                      uint64_t* __restrict__ y, int M, int K, int N, uint64_t mask, int wdigit, int accumulate) {
+                      uint64_t* __restrict__ y, int M, int K, int N, uint64_t mask, int wdigit, int accumulate,
+                      int w_vec) {
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM][kPitch];
   __shared__ __attribute__((aligned(16))) uint8_t w_lds[kBN][kPitch];
   __shared__ int csum[kThreads];
@@ -114,7 +115,7 @@ __global__ void __launch_bounds__(kThreads)
     if (WB == 8) {
       const int8_t* wrow = static_cast<const int8_t*>(wv) + size_t(n0 + wr) * K;
       const int kk = k0 + wk;
-      if (w_row_ok && kk + 32 <= K && ((K & 15) == 0)) {
+      if (w_row_ok && kk + 32 <= K && w_vec) {
         const uint4 a = *reinterpret_cast<const uint4*>(wrow + kk);
         const uint4 b = *reinterpret_cast<const uint4*>(wrow + kk + 16);
         wb[0] = a.x; wb[1] = a.y; wb[2] = a.z; wb[3] = a.w;
@@ -205,12 +206,14 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
                              int M, int K, int N, int mask_bits, hipStream_t s) {
   const uint64_t mask = mask_bits >= 64 ? ~0ull : ((1ull << mask_bits) - 1);
   const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(kThreads);
+  // 16-byte weight loads need 16-byte aligned rows
+  const int w_vec = (K % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
   if (w_bits == 8) {
-    hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, 0, 0);
+    hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, 0, 0, w_vec);
     return hipGetLastError();
   }
   for (int e = 0; e < 3; ++e) {
-    hipLaunchKernelGGL((share_gemm_kernel<32>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, e, e > 0);
+    hipLaunchKernelGGL((share_gemm_kernel<32>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, e, e > 0, 0);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }

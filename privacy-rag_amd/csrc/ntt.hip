@@ -10,37 +10,19 @@
 
 namespace praghip {
 
-// Raw loads of one limb in the layout the first pass of the transform uses:
-// forward - coalesced across threads; inverse - runs of 2^RSHORT consecutive
-// coefficients per (thread, block), read as 16-byte pairs.
-template <int LOGN, bool INV>
-__device__ __forceinline__ void load_limb(uint64_t (&r)[kE], const uint64_t* __restrict__ x, unsigned t) {
-  if (!INV) {
-#pragma unroll
-    for (int j = 0; j < kE; ++j) r[j] = x[fwd_in_index<LOGN>(t, j)];
-  } else {
-#pragma unroll
-    for (int j = 0; j < kE; j += 2) {
-      const ulonglong2 p = *reinterpret_cast<const ulonglong2*>(x + inv_in_index<LOGN>(t, j));
-      r[j] = p.x;
-      r[j + 1] = p.y;
-    }
-  }
-}
-
-// Transform of one limb: load, transform in registers + LDS, store.
+// Transform of one limb: coalesced loads in the first pass's layout, the
+// passes in registers + LDS, stores in the last pass's layout.
 template <int LOGN, bool INV, class A>
 __device__ __forceinline__ void transform_limb(uint64_t* __restrict__ x, const typename A::TW* __restrict__ tab,
-                                               const NttPrime& pr, typename A::T* lds) {
+                                               const NttPrime& pr, uint64_t* lds) {
   using T = typename A::T;
   const unsigned t = threadIdx.x;
   const A ar(pr);
-  uint64_t r[kE];
-  load_limb<LOGN, INV>(r, x, t);
   T v[kE];
 #pragma unroll
-  for (int j = 0; j < kE; ++j) v[j] = ar.from_u64(r[j]);
-  ntt_regs<LOGN, INV>(v, lds, t, tab, ar, pr);
+  for (int j = 0; j < kE; ++j)
+    v[j] = ar.from_u64(x[INV ? inv_in_index<LOGN>(t, j) : fwd_in_index<LOGN>(t, j)]);
+  ntt_regs<LOGN, INV>(v, reinterpret_cast<T*>(lds), t, tab, ar, pr, [&] {});
   if (!INV) {
 #pragma unroll
     for (int j = 0; j < kE; j += 2)
@@ -60,13 +42,12 @@ template <int LOGN, bool INV, class A>
 __global__ void __launch_bounds__(ntt_threads<LOGN>())
     ntt_kernel(uint64_t* __restrict__ data, size_t count, const NttPrime* __restrict__ primes,
                const typename A::TW* __restrict__ tw, int P, const int* __restrict__ sel, int C) {
-  __shared__ uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
+  __shared__ __attribute__((aligned(16))) uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
   for (size_t v = blockIdx.x; v < count; v += gridDim.x) {
     const size_t limb = (v / unsigned(C)) * unsigned(P) + unsigned(sel[v % unsigned(C)]);
     const int p = int(limb % unsigned(P));
     const NttPrime pr = primes[p];
-    transform_limb<LOGN, INV, A>(data + (limb << LOGN), tw + (size_t(p) << LOGN), pr,
-                                 reinterpret_cast<typename A::T*>(lds));
+    transform_limb<LOGN, INV, A>(data + (limb << LOGN), tw + (size_t(p) << LOGN), pr, lds);
   }
 }
 

@@ -106,11 +106,15 @@ struct ArF64 {
   static constexpr bool kAhead = true;  // load the next pass's twiddles one pass early
   double q, qinv;
   __device__ explicit ArF64(const NttPrime& p) : q(p.qd), qinv(p.qinv) {}
-  __device__ __forceinline__ T from_u64(uint64_t x) const { return (double)x; }
+  // Exact conversions for integers below 2^52: the bit pattern of 2^52 + x is
+  // 0x4330... with x in its 52 mantissa bits.
+  __device__ __forceinline__ T from_u64(uint64_t x) const {
+    return __longlong_as_double((long long)(x | 0x4330000000000000ull)) - 4503599627370496.0;
+  }
   __device__ __forceinline__ uint64_t to_u64(T x) const {
-    x = reduce_f64(x, q, qinv);
-    x = x < 0.0 ? x + q : x;
-    return (uint64_t)x;
+    x = reduce_f64(x, q, qinv);  // |x| <= q/2 + 1
+    x += x < 0.0 ? q + 4503599627370496.0 : 4503599627370496.0;
+    return (uint64_t)__double_as_longlong(x) & 0x000FFFFFFFFFFFFFull;
   }
   __device__ __forceinline__ uint64_t to_u64_fwd(T x) const { return to_u64(x); }
   __device__ __forceinline__ uint64_t to_u64_inv(T x) const { return to_u64(x); }
@@ -190,7 +194,7 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename 
           ar.fwd(v[j0], v[j1], w[n]);
         }
       }
-      if (s & 1) {
+      if ((s & 1) && s != LOGN - 1) {  // the final stage is reduced on output
 #pragma unroll
         for (int m = 0; m < (1 << R); ++m) ar.settle(v[(b << R) | m]);
       }
@@ -254,11 +258,14 @@ __device__ __forceinline__ void exchange(T (&v)[kE], T* lds, unsigned t) {
 
 // Pass P with its twiddles already in registers; loads pass P+1's twiddles
 // first, then computes, exchanges and recurses.
-template <int LOGN, bool INV, int P, class A>
+// `before_last` runs once the LDS is no longer needed by this limb (after the
+// last exchange, or at once for a single-pass transform).
+template <int LOGN, bool INV, int P, class A, class F>
 __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T* lds, unsigned t,
                                            const typename A::TW* __restrict__ tab, const A& ar,
                                            const NttPrime& pr,
-                                           const typename A::TW (&w)[pass_twiddles<Passes<LOGN>::r(INV, P)>()]) {
+                                           const typename A::TW (&w)[pass_twiddles<Passes<LOGN>::r(INV, P)>()],
+                                           F&& before_last) {
   using S = Passes<LOGN>;
   constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
   if constexpr (P + 1 < S::NP) {
@@ -271,8 +278,9 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
       fwd_pass<LOGN, LO, R>(v, w, ar);
     exchange<LOGN, LO, R, LO1, R1>(v, lds, t);
     if constexpr (!A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
-    run_passes<LOGN, INV, P + 1>(v, lds, t, tab, ar, pr, wn);
+    run_passes<LOGN, INV, P + 1>(v, lds, t, tab, ar, pr, wn, before_last);
   } else {
+    before_last();
     if constexpr (INV)
       inv_pass<LOGN, LO, R>(v, w, ar, pr);
     else
@@ -282,13 +290,19 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
 
 // Whole-limb transform on register data (v holds the input layout on entry
 // and the output layout on exit; values stay in the policy's lazy form).
-template <int LOGN, bool INV, class A>
+template <int LOGN, bool INV, class A, class F>
 __device__ __forceinline__ void ntt_regs(typename A::T (&v)[kE], typename A::T* lds, unsigned t,
-                                         const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr) {
+                                         const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr,
+                                         F&& before_last) {
   using S = Passes<LOGN>;
   typename A::TW w0[pass_twiddles<S::r(INV, 0)>()];
   load_pass_twiddles<LOGN, S::lo(INV, 0), S::r(INV, 0), INV>(w0, t, tab);
-  run_passes<LOGN, INV, 0>(v, lds, t, tab, ar, pr, w0);
+  run_passes<LOGN, INV, 0>(v, lds, t, tab, ar, pr, w0, before_last);
+}
+template <int LOGN, bool INV, class A>
+__device__ __forceinline__ void ntt_regs(typename A::T (&v)[kE], typename A::T* lds, unsigned t,
+                                         const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr) {
+  ntt_regs<LOGN, INV>(v, lds, t, tab, ar, pr, [] {});
 }
 
 // Register layouts at the boundaries of a transform.

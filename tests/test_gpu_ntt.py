@@ -154,3 +154,13 @@ def test_ntt_host_api_and_errors(gpu):
     with pytest.raises(praghip.PraghipError) as e:
         plan.transform(a)
     assert "E_NTT_CLOSED" in e.value.text
+
+
+def test_ntt_rejects_misaligned_device_buffer(gpu):
+    import torch
+    plan = praghip.NttBatch(C2, 14)
+    buf = torch.zeros(16384 + 1, dtype=torch.int64, device="cuda")
+    with pytest.raises(praghip.PraghipError) as e:
+        plan.forward(buf[1:])  # 8-byte aligned view
+    assert "E_NTT_ALIGNMENT" in e.value.text
+    assert torch.count_nonzero(buf) == 0  # nothing was launched
