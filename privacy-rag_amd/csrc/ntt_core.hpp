@@ -12,8 +12,8 @@
 // pass's access pattern free of bank conflicts).
 //
 // Twiddles: a pass's twiddles are loaded into registers in one batch - for the
-// float path while the previous pass computes, so their L2 latency hides
-// behind a whole pass of arithmetic; for the integer path (16-byte pairs, too
+// float path halfway through the previous pass, so their L2 latency hides
+// behind half a pass of arithmetic; for the integer path (16-byte pairs, too
 // many registers to hold two passes) at the start of the pass, one wait per
 // pass.
 //
@@ -40,7 +40,7 @@ struct NttPrime {
   int pad;
 };
 
-__device__ __forceinline__ unsigned lds_pos(unsigned x) { return x + (x >> 4); }
+__host__ __device__ __forceinline__ unsigned lds_pos(unsigned x) { return x + (x >> 4); }
 
 constexpr int kLogE = 4;  // 16 coefficients per thread
 constexpr int kE = 1 << kLogE;
@@ -50,7 +50,7 @@ constexpr int kE = 1 << kLogE;
 // blocks; block b acts as thread t + b*THREADS, so consecutive threads stay on
 // consecutive coefficients whenever LO > 0.
 template <int LOGN, int LO, int R>
-__device__ __forceinline__ unsigned elem_index(unsigned t, int j) {
+__host__ __device__ __forceinline__ unsigned elem_index(unsigned t, int j) {
   constexpr unsigned THREADS = (1u << LOGN) >> kLogE;
   const int b = j >> R, jl = j & ((1 << R) - 1);
   const unsigned T = t + unsigned(b) * THREADS;
@@ -176,9 +176,17 @@ __device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<R>()], 
 
 // Forward radix-2^R pass over gap bits [LO, LO+R): global stages
 // s = LOGN-LO-R .. LOGN-LO-1.
-template <int LOGN, int LO, int R, class A>
+// A pass calls `mid` once, halfway through its butterflies (after stage R/2-1
+// of a single block, or after block SUB/2-1): the twiddles of the early stages
+// are dead by then, which is where the next pass's twiddle loads go.
+template <int R>
+__device__ __forceinline__ constexpr bool is_mid(int b, int i) {
+  return (kE >> R) == 1 ? (i == R / 2 - 1) : (b == (kE >> R) / 2 - 1 && i == R - 1);
+}
+
+template <int LOGN, int LO, int R, class A, class F>
 __device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename A::TW (&w)[pass_twiddles<R>()],
-                                         const A& ar) {
+                                         const A& ar, F&& mid) {
   constexpr int SUB = kE >> R;
   int n = 0;
 #pragma unroll
@@ -198,14 +206,15 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename 
 #pragma unroll
         for (int m = 0; m < (1 << R); ++m) ar.settle(v[(b << R) | m]);
       }
+      if (is_mid<R>(b, i)) mid();
     }
   }
 }
 
 // Inverse radix-2^R pass over gap bits [LO, LO+R): stages l = LO .. LO+R-1.
-template <int LOGN, int LO, int R, class A>
+template <int LOGN, int LO, int R, class A, class F>
 __device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename A::TW (&w)[pass_twiddles<R>()],
-                                         const A& ar, const NttPrime& pr) {
+                                         const A& ar, const NttPrime& pr, F&& mid) {
   constexpr int SUB = kE >> R;
   int n = 0;
 #pragma unroll
@@ -224,6 +233,7 @@ __device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename 
             ar.inv(v[j0], v[j1], w[n]);
         }
       }
+      if (is_mid<R>(b, i)) mid();
     }
   }
 }
@@ -246,13 +256,31 @@ struct Passes {
   static constexpr int r(bool inv, int p) { return inv ? inv_r(p) : fwd_r(p); }
 };
 
+// Offset of register j from register 0 in a pass's padded LDS slots.  The
+// index of register j is elem_index(t, 0) + d(j) with d(j) made of whole
+// fields (jl << LO, b * THREADS << R) that never carry into bit 4 when added
+// to elem_index(t, 0) (THREADS is a multiple of 2^LO, and the low four bits of
+// the two summands occupy disjoint positions), so lds_pos(index) =
+// lds_pos(elem_index(t, 0)) + d(j) + (d(j) >> 4): one base register per pass
+// and compile-time offsets, instead of 16 per-thread addresses the compiler
+// would otherwise keep live across the limb loop.
+template <int LOGN, int LO, int R>
+__host__ __device__ constexpr unsigned slot_offset(int j) {
+  constexpr unsigned THREADS = (1u << LOGN) >> kLogE;
+  const unsigned b = unsigned(j) >> R, jl = unsigned(j) & ((1u << R) - 1);
+  const unsigned d = ((b * THREADS) << R) + (jl << LO);
+  return d + (d >> 4);
+}
+
 template <int LOGN, int LO0, int R0, int LO1, int R1, class T>
 __device__ __forceinline__ void exchange(T (&v)[kE], T* lds, unsigned t) {
+  T* wbase = lds + lds_pos(elem_index<LOGN, LO0, R0>(t, 0));
 #pragma unroll
-  for (int j = 0; j < kE; ++j) lds[lds_pos(elem_index<LOGN, LO0, R0>(t, j))] = v[j];
+  for (int j = 0; j < kE; ++j) wbase[slot_offset<LOGN, LO0, R0>(j)] = v[j];
   __syncthreads();
+  const T* rbase = lds + lds_pos(elem_index<LOGN, LO1, R1>(t, 0));
 #pragma unroll
-  for (int j = 0; j < kE; ++j) v[j] = lds[lds_pos(elem_index<LOGN, LO1, R1>(t, j))];
+  for (int j = 0; j < kE; ++j) v[j] = rbase[slot_offset<LOGN, LO1, R1>(j)];
   __syncthreads();
 }
 
@@ -271,20 +299,22 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
   if constexpr (P + 1 < S::NP) {
     constexpr int LO1 = S::lo(INV, P + 1), R1 = S::r(INV, P + 1);
     typename A::TW wn[pass_twiddles<R1>()];
-    if constexpr (A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
+    auto prefetch = [&] {
+      if constexpr (A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
+    };
     if constexpr (INV)
-      inv_pass<LOGN, LO, R>(v, w, ar, pr);
+      inv_pass<LOGN, LO, R>(v, w, ar, pr, prefetch);
     else
-      fwd_pass<LOGN, LO, R>(v, w, ar);
+      fwd_pass<LOGN, LO, R>(v, w, ar, prefetch);
     exchange<LOGN, LO, R, LO1, R1>(v, lds, t);
     if constexpr (!A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
     run_passes<LOGN, INV, P + 1>(v, lds, t, tab, ar, pr, wn, before_last);
   } else {
     before_last();
     if constexpr (INV)
-      inv_pass<LOGN, LO, R>(v, w, ar, pr);
+      inv_pass<LOGN, LO, R>(v, w, ar, pr, [] {});
     else
-      fwd_pass<LOGN, LO, R>(v, w, ar);
+      fwd_pass<LOGN, LO, R>(v, w, ar, [] {});
   }
 }
 
