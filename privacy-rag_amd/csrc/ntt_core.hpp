@@ -45,19 +45,6 @@ __host__ __device__ __forceinline__ unsigned lds_pos(unsigned x) { return x + (x
 constexpr int kLogE = 4;  // 16 coefficients per thread
 constexpr int kE = 1 << kLogE;
 
-// Index of the j-th register coefficient of thread t in a pass over the gap
-// bits [LO, LO+R).  When R < 4 each thread runs 16>>R independent radix-2^R
-// blocks; block b acts as thread t + b*THREADS, so consecutive threads stay on
-// consecutive coefficients whenever LO > 0.
-template <int LOGN, int LO, int R>
-__host__ __device__ __forceinline__ unsigned elem_index(unsigned t, int j) {
-  constexpr unsigned THREADS = (1u << LOGN) >> kLogE;
-  const int b = j >> R, jl = j & ((1 << R) - 1);
-  const unsigned T = t + unsigned(b) * THREADS;
-  const unsigned lo = T & ((1u << LO) - 1), hi = T >> LO;
-  return (hi << (LO + R)) | (unsigned(jl) << LO) | lo;
-}
-
 // ---------------------------------------------------------------- policies
 struct ArU64 {
   using T = uint64_t;
@@ -138,24 +125,107 @@ struct ArF64 {
   __device__ __forceinline__ void settle(T& x) const { x = reduce_f64(x, q, qinv); }
 };
 
+// Pass geometry.  Forward passes take 4 gap bits from the top down, the last
+// one the remainder [0, RSHORT); inverse passes start with the remainder
+// [0, RSHORT) and continue upwards 4 bits at a time.
+template <int LOGN>
+struct Passes {
+  static constexpr int NP = (LOGN + kLogE - 1) / kLogE;
+  static constexpr int RSHORT = LOGN - kLogE * (NP - 1);
+  static constexpr int fwd_lo(int p) { return p < NP - 1 ? LOGN - kLogE * (p + 1) : 0; }
+  static constexpr int fwd_r(int p) { return p < NP - 1 ? kLogE : RSHORT; }
+  static constexpr int inv_lo(int p) { return p == 0 ? 0 : RSHORT + kLogE * (p - 1); }
+  static constexpr int inv_r(int p) { return p == 0 ? RSHORT : kLogE; }
+  static constexpr int lo(bool inv, int p) { return inv ? inv_lo(p) : fwd_lo(p); }
+  static constexpr int r(bool inv, int p) { return inv ? inv_r(p) : fwd_r(p); }
+  static constexpr int LANE_BITS = LOGN - kLogE < 6 ? LOGN - kLogE : 6;  // thread bits inside a wave
+  static constexpr int WAVE_BITS = LOGN - kLogE - LANE_BITS;             // thread bits naming the wave
+};
+
+// Placement of a thread's 16 registers in a pass.  The coefficient index is
+// assembled from three fields:
+//   register bits - the pass's gap bits [LO, LO+R), and when R < 4 (LO = 0
+//                   then) 4 - R bits just below the wave bits for the
+//                   independent blocks;
+//   wave bits     - the top WAVE_BITS bits, except in the pass whose gap bits
+//                   are the top bits, where they sit just below them;
+//   lane bits     - every other bit, in increasing order.
+// With the wave bits fixed to the top in all but one pass, a wave owns the
+// same contiguous 2^(LOGN - WAVE_BITS) coefficients in consecutive passes, so those
+// exchanges stay inside the wave (its own LDS region, no workgroup barrier);
+// only the exchange into or out of the top pass crosses waves.  The first
+// forward pass and the last inverse pass put consecutive lanes on consecutive
+// coefficients (coalesced global access); the last forward and first inverse
+// pass give each lane runs of 2^R consecutive coefficients, consecutive lanes
+// on consecutive runs.
+template <int LOGN, bool INV, int P>
+struct PassMap {
+  using S = Passes<LOGN>;
+  static constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
+  static constexpr int WAVE_LO = (LO + R == LOGN) ? LO - S::WAVE_BITS : LOGN - S::WAVE_BITS;
+  // block bits (R < 4, LO = 0): just below the wave bits
+  static constexpr int BLOCK_LO = WAVE_LO - (kLogE - R);
+  static constexpr int reg_bit(int q) { return q < R ? LO + q : BLOCK_LO + (q - R); }
+  static constexpr bool is_reg(int e) { return (e >= LO && e < LO + R) || (e >= BLOCK_LO && e < WAVE_LO && R < kLogE); }
+  static constexpr bool is_wave(int e) { return e >= WAVE_LO && e < WAVE_LO + S::WAVE_BITS; }
+  static constexpr int lane_bit(int q) {
+    int c = 0;
+    for (int e = 0; e < LOGN; ++e)
+      if (!is_reg(e) && !is_wave(e)) {
+        if (c == q) return e;
+        ++c;
+      }
+    return -1;
+  }
+  // every lane bit lies below the gap bits: the bits above them (the twiddle
+  // group) are the same for all lanes of a wave
+  static constexpr bool uniform_groups() {
+    for (int q = 0; q < S::LANE_BITS; ++q)
+      if (lane_bit(q) >= LO + R) return false;
+    return true;
+  }
+  __host__ __device__ static constexpr unsigned reg_field(int j) {
+    unsigned x = 0;
+    for (int q = 0; q < kLogE; ++q) x |= unsigned((j >> q) & 1) << reg_bit(q);
+    return x;
+  }
+  __host__ __device__ static unsigned thread_field(unsigned t) {
+    unsigned x = 0;
+#pragma unroll
+    for (int q = 0; q < S::LANE_BITS; ++q) x |= ((t >> q) & 1u) << lane_bit(q);
+#pragma unroll
+    for (int q = 0; q < S::WAVE_BITS; ++q) x |= ((t >> (6 + q)) & 1u) << (WAVE_LO + q);
+    return x;
+  }
+  __host__ __device__ static unsigned elem(unsigned t, int j) { return thread_field(t) | reg_field(j); }
+  // padded LDS slot of register j relative to register 0: the fields are
+  // disjoint, so the sum never carries into bit 4 and lds_pos is linear
+  __host__ __device__ static constexpr unsigned slot_offset(int j) {
+    const unsigned d = reg_field(j);
+    return d + (d >> 4);
+  }
+};
+
 // ------------------------------------------------------------------ passes
 // Twiddles of one pass: SUB blocks x (2^R - 1) entries, in the order the pass
 // consumes them (block, stage, group).
 template <int R>
 constexpr int pass_twiddles() { return (kE >> R) * ((1 << R) - 1); }
 
-template <int LOGN, int LO, int R, bool INV, class TW>
-__device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<R>()], unsigned t,
+template <int LOGN, bool INV, int P, class TW>
+__device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<Passes<LOGN>::r(INV, P)>()], unsigned t,
                                                    const TW* __restrict__ tab) {
-  constexpr int SUB = kE >> R;
-  constexpr unsigned N = 1u << LOGN, THREADS = N >> kLogE;
+  using M = PassMap<LOGN, INV, P>;
+  constexpr int LO = M::LO, R = M::R, SUB = kE >> R;
+  constexpr unsigned N = 1u << LOGN;
   int n = 0;
 #pragma unroll
   for (int b = 0; b < SUB; ++b) {
-    // With LO >= 6 all 64 lanes of a wave share hi: the twiddle addresses are
-    // wave-uniform and the loads go through the scalar unit into SGPRs.
-    const unsigned hi_lane = (t + unsigned(b) * THREADS) >> LO;
-    const unsigned hi = LO >= 6 ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
+    // group index of the block: the coefficient bits above the gap bits.
+    // When no lane bit lies there, all lanes of a wave share it and the
+    // twiddle loads go through the scalar unit into SGPRs.
+    const unsigned hi_lane = M::elem(t, b << R) >> (LO + R);
+    const unsigned hi = M::uniform_groups() ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (!INV) {
@@ -238,50 +308,31 @@ __device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename 
   }
 }
 
-// Pass geometry.  Forward passes take 4 gap bits from the top down, the last
-// one the remainder [0, RSHORT); inverse passes start with the remainder
-// [0, RSHORT) and continue upwards 4 bits at a time.  With that order the
-// forward input and inverse output are coalesced across threads, and the
-// forward output / inverse input come as 2^RSHORT consecutive coefficients per
-// (thread, block).
-template <int LOGN>
-struct Passes {
-  static constexpr int NP = (LOGN + kLogE - 1) / kLogE;
-  static constexpr int RSHORT = LOGN - kLogE * (NP - 1);
-  static constexpr int fwd_lo(int p) { return p < NP - 1 ? LOGN - kLogE * (p + 1) : 0; }
-  static constexpr int fwd_r(int p) { return p < NP - 1 ? kLogE : RSHORT; }
-  static constexpr int inv_lo(int p) { return p == 0 ? 0 : RSHORT + kLogE * (p - 1); }
-  static constexpr int inv_r(int p) { return p == 0 ? RSHORT : kLogE; }
-  static constexpr int lo(bool inv, int p) { return inv ? inv_lo(p) : fwd_lo(p); }
-  static constexpr int r(bool inv, int p) { return inv ? inv_r(p) : fwd_r(p); }
-};
-
-// Offset of register j from register 0 in a pass's padded LDS slots.  The
-// index of register j is elem_index(t, 0) + d(j) with d(j) made of whole
-// fields (jl << LO, b * THREADS << R) that never carry into bit 4 when added
-// to elem_index(t, 0) (THREADS is a multiple of 2^LO, and the low four bits of
-// the two summands occupy disjoint positions), so lds_pos(index) =
-// lds_pos(elem_index(t, 0)) + d(j) + (d(j) >> 4): one base register per pass
-// and compile-time offsets, instead of 16 per-thread addresses the compiler
-// would otherwise keep live across the limb loop.
-template <int LOGN, int LO, int R>
-__host__ __device__ constexpr unsigned slot_offset(int j) {
-  constexpr unsigned THREADS = (1u << LOGN) >> kLogE;
-  const unsigned b = unsigned(j) >> R, jl = unsigned(j) & ((1u << R) - 1);
-  const unsigned d = ((b * THREADS) << R) + (jl << LO);
-  return d + (d >> 4);
-}
-
-template <int LOGN, int LO0, int R0, int LO1, int R1, class T>
+// Exchange between consecutive passes.  When both passes give the wave the
+// same coefficients (same wave bits) the exchange stays in the wave's own LDS
+// region: LDS operations of one wave execute in order, so only a compiler
+// barrier is needed.  Otherwise the whole workgroup synchronises before (other
+// waves may still read their regions), between, and after.
+template <int LOGN, bool INV, int P, class T>
 __device__ __forceinline__ void exchange(T (&v)[kE], T* lds, unsigned t) {
-  T* wbase = lds + lds_pos(elem_index<LOGN, LO0, R0>(t, 0));
+  using A = PassMap<LOGN, INV, P>;
+  using B = PassMap<LOGN, INV, P + 1>;
+  constexpr bool in_wave = A::WAVE_LO == B::WAVE_LO || Passes<LOGN>::WAVE_BITS == 0;
+  if constexpr (!in_wave) __syncthreads();
+  T* wbase = lds + lds_pos(A::elem(t, 0));
 #pragma unroll
-  for (int j = 0; j < kE; ++j) wbase[slot_offset<LOGN, LO0, R0>(j)] = v[j];
-  __syncthreads();
-  const T* rbase = lds + lds_pos(elem_index<LOGN, LO1, R1>(t, 0));
+  for (int j = 0; j < kE; ++j) wbase[A::slot_offset(j)] = v[j];
+  if constexpr (in_wave)
+    __builtin_amdgcn_wave_barrier();
+  else
+    __syncthreads();
+  const T* rbase = lds + lds_pos(B::elem(t, 0));
 #pragma unroll
-  for (int j = 0; j < kE; ++j) v[j] = rbase[slot_offset<LOGN, LO1, R1>(j)];
-  __syncthreads();
+  for (int j = 0; j < kE; ++j) v[j] = rbase[B::slot_offset(j)];
+  if constexpr (in_wave)
+    __builtin_amdgcn_wave_barrier();
+  else
+    __syncthreads();
 }
 
 // Pass P with its twiddles already in registers; loads pass P+1's twiddles
@@ -300,14 +351,14 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
     constexpr int LO1 = S::lo(INV, P + 1), R1 = S::r(INV, P + 1);
     typename A::TW wn[pass_twiddles<R1>()];
     auto prefetch = [&] {
-      if constexpr (A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
+      if constexpr (A::kAhead) load_pass_twiddles<LOGN, INV, P + 1>(wn, t, tab);
     };
     if constexpr (INV)
       inv_pass<LOGN, LO, R>(v, w, ar, pr, prefetch);
     else
       fwd_pass<LOGN, LO, R>(v, w, ar, prefetch);
-    exchange<LOGN, LO, R, LO1, R1>(v, lds, t);
-    if constexpr (!A::kAhead) load_pass_twiddles<LOGN, LO1, R1, INV>(wn, t, tab);
+    exchange<LOGN, INV, P>(v, lds, t);
+    if constexpr (!A::kAhead) load_pass_twiddles<LOGN, INV, P + 1>(wn, t, tab);
     run_passes<LOGN, INV, P + 1>(v, lds, t, tab, ar, pr, wn, before_last);
   } else {
     before_last();
@@ -326,7 +377,7 @@ __device__ __forceinline__ void ntt_regs(typename A::T (&v)[kE], typename A::T* 
                                          F&& before_last) {
   using S = Passes<LOGN>;
   typename A::TW w0[pass_twiddles<S::r(INV, 0)>()];
-  load_pass_twiddles<LOGN, S::lo(INV, 0), S::r(INV, 0), INV>(w0, t, tab);
+  load_pass_twiddles<LOGN, INV, 0>(w0, t, tab);
   run_passes<LOGN, INV, 0>(v, lds, t, tab, ar, pr, w0, before_last);
 }
 template <int LOGN, bool INV, class A>
@@ -337,24 +388,16 @@ __device__ __forceinline__ void ntt_regs(typename A::T (&v)[kE], typename A::T* 
 
 // Register layouts at the boundaries of a transform.
 template <int LOGN>
-__device__ __forceinline__ unsigned fwd_in_index(unsigned t, int j) {
-  using S = Passes<LOGN>;
-  return elem_index<LOGN, S::fwd_lo(0), S::fwd_r(0)>(t, j);
-}
+__device__ __forceinline__ unsigned fwd_in_index(unsigned t, int j) { return PassMap<LOGN, false, 0>::elem(t, j); }
 template <int LOGN>
 __device__ __forceinline__ unsigned fwd_out_index(unsigned t, int j) {
-  using S = Passes<LOGN>;
-  return elem_index<LOGN, S::fwd_lo(S::NP - 1), S::fwd_r(S::NP - 1)>(t, j);
+  return PassMap<LOGN, false, Passes<LOGN>::NP - 1>::elem(t, j);
 }
 template <int LOGN>
-__device__ __forceinline__ unsigned inv_in_index(unsigned t, int j) {
-  using S = Passes<LOGN>;
-  return elem_index<LOGN, S::inv_lo(0), S::inv_r(0)>(t, j);
-}
+__device__ __forceinline__ unsigned inv_in_index(unsigned t, int j) { return PassMap<LOGN, true, 0>::elem(t, j); }
 template <int LOGN>
 __device__ __forceinline__ unsigned inv_out_index(unsigned t, int j) {
-  using S = Passes<LOGN>;
-  return elem_index<LOGN, S::inv_lo(S::NP - 1), S::inv_r(S::NP - 1)>(t, j);
+  return PassMap<LOGN, true, Passes<LOGN>::NP - 1>::elem(t, j);
 }
 
 template <int LOGN>

@@ -1,34 +1,67 @@
-// CPU check of the NTT LDS layout: for every pass of every transform size,
-// lds_pos(elem_index(t, j)) == lds_pos(elem_index(t, 0)) + slot_offset(j), and
-// every slot stays inside the N + N/16 padded buffer.
-#include "ntt_core.hpp"
+// CPU check of the NTT register/LDS layout (PassMap in ntt_core.hpp), for every
+// pass of every transform size:
+//   - elem(t, j) is a bijection onto [0, N);
+//   - lds_pos(elem(t, j)) == lds_pos(elem(t, 0)) + slot_offset(j), inside the
+//     N + N/16 padded buffer;
+//   - when uniform_groups() holds, the twiddle group (bits above the gap bits)
+//     is the same for all lanes of a wave;
+//   - consecutive passes with equal wave bits give each wave the same
+//     coefficients (their exchange stays inside the wave).
 #include <cstdio>
+#include <vector>
+
+#include "ntt_core.hpp"
 using namespace praghip;
-template <int LOGN, int LO, int R> int check() {
-  constexpr unsigned THREADS = (1u << LOGN) >> kLogE;
-  int bad = 0; unsigned maxpos = 0;
+
+template <int LOGN, bool INV, int P>
+int check_pass() {
+  using M = PassMap<LOGN, INV, P>;
+  constexpr unsigned N = 1u << LOGN, THREADS = N >> kLogE, LIMIT = N + N / 16;
+  std::vector<int> seen(N, 0);
+  int bad = 0;
   for (unsigned t = 0; t < THREADS; ++t)
     for (int j = 0; j < kE; ++j) {
-      unsigned a = lds_pos(elem_index<LOGN, LO, R>(t, j));
-      unsigned b = lds_pos(elem_index<LOGN, LO, R>(t, 0)) + slot_offset<LOGN, LO, R>(j);
-      if (a != b) ++bad;
-      if (b > maxpos) maxpos = b;
+      const unsigned x = M::elem(t, j);
+      if (x >= N) { ++bad; continue; }
+      seen[x]++;
+      if (lds_pos(x) != lds_pos(M::elem(t, 0)) + M::slot_offset(j) || lds_pos(x) >= LIMIT) ++bad;
+      // element bits in the gap window must come from the register index
+      if (((x >> M::LO) & ((1u << M::R) - 1)) != (unsigned(j) & ((1u << M::R) - 1))) ++bad;
     }
-  printf("LOGN=%d LO=%d R=%d bad=%d maxpos=%u limit=%u\n", LOGN, LO, R, bad, maxpos, (1u << LOGN) + (1u << LOGN) / 16);
-  return bad + (maxpos >= (1u << LOGN) + (1u << LOGN) / 16);
-}
-template <int LOGN> int all() {
-  using S = Passes<LOGN>;
-  int bad = 0;
-  bad += check<LOGN, S::fwd_lo(0), S::fwd_r(0)>();
-  if constexpr (S::NP > 1) bad += check<LOGN, S::fwd_lo(1), S::fwd_r(1)>() + check<LOGN, S::inv_lo(1), S::inv_r(1)>();
-  if constexpr (S::NP > 2) bad += check<LOGN, S::fwd_lo(2), S::fwd_r(2)>() + check<LOGN, S::inv_lo(2), S::inv_r(2)>();
-  if constexpr (S::NP > 3) bad += check<LOGN, S::fwd_lo(3), S::fwd_r(3)>() + check<LOGN, S::inv_lo(3), S::inv_r(3)>();
-  bad += check<LOGN, S::inv_lo(0), S::inv_r(0)>();
+  for (unsigned x = 0; x < N; ++x) bad += seen[x] != 1;
+  if (M::uniform_groups())
+    for (unsigned t = 0; t < THREADS; ++t)
+      for (int b = 0; b < (kE >> M::R); ++b)
+        if ((M::elem(t, b << M::R) >> (M::LO + M::R)) != (M::elem(t & ~63u, b << M::R) >> (M::LO + M::R))) ++bad;
+  if constexpr (P + 1 < Passes<LOGN>::NP) {
+    using B = PassMap<LOGN, INV, P + 1>;
+    if (M::WAVE_LO == B::WAVE_LO)
+      for (unsigned t = 0; t < THREADS; ++t) {
+        const unsigned w = t >> 6;
+        for (int j = 0; j < kE; ++j) {
+          // the coefficient t holds after the exchange belongs to wave w before it
+          const unsigned x = B::elem(t, j);
+          bool found = false;
+          for (unsigned l = 0; l < 64 && (w * 64 + l) < THREADS && !found; ++l)
+            for (int j2 = 0; j2 < kE && !found; ++j2) found = M::elem(w * 64 + l, j2) == x;
+          if (!found) ++bad;
+        }
+      }
+    bad += check_pass<LOGN, INV, P + 1>();
+  }
+  if (bad) printf("LOGN=%d INV=%d pass=%d: %d violations\n", LOGN, int(INV), P, bad);
   return bad;
 }
+
+template <int LOGN>
+int check_size() {
+  return check_pass<LOGN, false, 0>() + check_pass<LOGN, true, 0>();
+}
+
 int main() {
-  int bad = all<4>() + all<5>() + all<6>() + all<7>() + all<8>() + all<9>() + all<10>() + all<11>() + all<12>() + all<13>() + all<14>();
+  const int bad = check_size<4>() + check_size<5>() + check_size<6>() + check_size<7>() + check_size<8>() +
+                  check_size<9>() + check_size<10>() + check_size<11>() + check_size<12>() + check_size<13>() +
+                  check_size<14>();
   printf(bad ? "FAIL\n" : "ALL OK\n");
   return bad != 0;
 }
