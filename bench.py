@@ -1,10 +1,10 @@
 """Benchmark of the BFV hot path on one MI355X.
 
-Primary line (the workload BASELINE's metric is quoted on): batched forward +
-inverse negacyclic NTT at N=16384 over six ~50-bit primes, 256 ciphertexts x 2
-polynomials = 3072 limbs (one step = one forward and one inverse launch over
-all limbs).  Also reported in the same JSON line: the C3 keyswitch (dnum=3,
-64 ciphertexts, 64 independent keys) and the C4 share GEMM (512x1024x3072,
+Primary line: batched forward + inverse negacyclic NTT at N=16384 over six
+~50-bit primes, 256 ciphertexts x 2 polynomials = 3072 limbs (one step = one
+forward and one inverse launch over all limbs).  Also reported in the same
+JSON line: the keyswitch at N=16384, L=6 + 1 special prime (dnum=3, 64
+ciphertexts, 64 independent keys) and the share GEMM (512x1024x3072,
 int8 weights, mod 2^64).  Inputs are generated on the GPU and are resident in
 HBM before timing; every timed result is checked afterwards (round trip,
 re-run equality) and a slice is compared with the oracle.
@@ -33,6 +33,22 @@ N = 16384
 LOG_N = 14
 
 
+def measured_traffic(workload: str, launches_per_step: int):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (profiles/hbm_traffic.json), scaled by the copy calibration; None
+    when no summary is committed for the workload."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    if workload not in t:
+        return None
+    fs, ws = t["calibration"]["fetch_scale"], t["calibration"]["write_scale"]
+    total = sum(fs * k["FETCH_SIZE_KiB"] + ws * k["WRITE_SIZE_KiB"] for k in t[workload]["kernels"].values())
+    return int(total * 1024 / launches_per_step)
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -59,7 +75,7 @@ class Timer:
 
 def bench_ntt(torch, praghip, steps, warmup):
     from praghip import params, synth
-    q = params.c2_primes()
+    q = params.primes_n16384_50bit()
     limbs = 256 * 2 * 6
     data = torch.empty(limbs * N, dtype=torch.int64, device="cuda")
     synth.fill_residues(data, q, LOG_N, 0x5052414700000002)
@@ -79,7 +95,7 @@ def bench_ntt(torch, praghip, steps, warmup):
         "limbs": limbs, "q": q, "ms_per_step": ms, "launch_ms": launch_ms,
         "ntt_per_s": 2 * limbs / (ms * 1e-3), "poly_ntt_per_s": 2 * limbs / 6 / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("ntt", 2),
                      "kernel": "ntt_kernel<14> (forward and inverse launches)",
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
@@ -87,7 +103,7 @@ def bench_ntt(torch, praghip, steps, warmup):
 
 def bench_keyswitch(torch, praghip, steps, warmup):
     from praghip import params, synth
-    q = params.c3_primes()
+    q = params.primes_n16384_switch()
     L, dnum, batch = 6, 3, 64
     sw = praghip.Switch(q, LOG_N, dnum, max_batch=batch)
     ct = torch.empty(batch * 2 * L * N, dtype=torch.int64, device="cuda")
@@ -109,8 +125,10 @@ def bench_keyswitch(torch, praghip, steps, warmup):
     return {
         "batch": batch, "dnum": dnum, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole keyswitch (ModUp, NTT, product, INTT, ModDown)",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("keyswitch", 1),
+                     "kernel": "whole keyswitch batch (all its launches); traffic is per batch",
+                     "algorithmic_bytes_per_batch": batch * bytes_per_ks,
                      "algorithmic_bytes_per_keyswitch": bytes_per_ks},
         "_tensors": (ct, keys, out, q),
     }
@@ -134,7 +152,7 @@ def bench_gemm(torch, praghip, steps, warmup):
     return {
         "shape": [m, k, n], "ms_per_step": ms, "tops": tops,
         "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": None,
+                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm", 1),
                      "kernel": "share_gemm_kernel<8> (i8 MFMA ops executed)"},
         "_tensors": (x, w, y),
     }
@@ -158,7 +176,7 @@ def cpu_baselines(torch, res, budget_s: float):
     import oracle
     threads = len(os.sched_getaffinity(0))
     out = {}
-    # NTT: sample of the C2 batch, all host threads
+    # NTT: sample of the 3072-limb batch, all host threads
     q = res["ntt"]["q"]
     tab = oracle.Tables(q, LOG_N)
     limbs = 384
@@ -173,8 +191,8 @@ def cpu_baselines(torch, res, budget_s: float):
         oracle.ntt(oracle.ntt(a, tab, threads=threads), tab, inverse=True, threads=threads)
     dt = (time.perf_counter() - t0) / reps
     out["ntt"] = {"value": 2 * limbs / dt, "unit": "limb-NTT/s", "cores": threads, "kind": "port",
-                  "sample": f"{limbs} limbs of the C2 batch, forward+inverse, x{reps}"}
-    # keyswitch: 4 ciphertexts of C3 with their keys
+                  "sample": f"{limbs} limbs of the 3072-limb N=16384 batch, forward+inverse, x{reps}"}
+    # keyswitch: a few of the 64 ciphertexts with their keys
     ct_t, keys_t, out_t, q3 = res["keyswitch"]["_tensors"]
     nb = 2 * threads if threads <= 8 else threads
     nb = min(nb, 64)
@@ -188,8 +206,8 @@ def cpu_baselines(torch, res, budget_s: float):
     gpu_slice = out_t[: nb * 2 * 6 * N].cpu().numpy().view(np.uint64).reshape(nb, 2, 6, N)
     out["keyswitch_parity"] = bool(np.array_equal(got, gpu_slice))
     out["keyswitch"] = {"value": nb / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
-                        "sample": f"{nb} C3 ciphertexts (dnum=3) with their own keys"}
-    # GEMM: 64 rows of the C4 activations against all 3072 weight rows
+                        "sample": f"{nb} of the 64 N=16384 ciphertexts (dnum=3) with their own keys"}
+    # GEMM: 64 rows of the 512x1024 activations against all 3072 weight rows
     x_t, w_t, y_t = res["gemm"]["_tensors"]
     rows = 64
     x = x_t[:rows].cpu().numpy().view(np.uint64)
@@ -230,15 +248,15 @@ def main() -> int:
                           "higher_is_better": True, "bytes_each_way": r["bytes_each_way"]}), flush=True)
         return 0
     if args.only in ("all", "ntt"):
-        log("NTT C2 ...")
+        log("NTT N=16384, 3072 limbs ...")
         res["ntt"] = bench_ntt(torch, praghip, args.steps, args.warmup)
         log(f"NTT {res['ntt']['ntt_per_s']:.4g} limb-NTT/s, {res['ntt']['roofline']['achieved']} GB/s")
     if args.only in ("all", "keyswitch"):
-        log("keyswitch C3 ...")
+        log("keyswitch N=16384 dnum=3, 64 ciphertexts ...")
         res["keyswitch"] = bench_keyswitch(torch, praghip, args.steps, args.warmup)
         log(f"keyswitch {res['keyswitch']['keyswitch_per_s']:.4g}/s")
     if args.only in ("all", "gemm"):
-        log("share GEMM C4 ...")
+        log("share GEMM 512x1024x3072 ...")
         res["gemm"] = bench_gemm(torch, praghip, args.steps, args.warmup)
         log(f"GEMM {res['gemm']['tops']:.4g} TOPS")
     cpu = {}
@@ -269,10 +287,10 @@ def main() -> int:
         "dtype": "f64" if key == "ntt" else ("u64+f64" if key == "keyswitch" else "i8"),
         "data": "synthetic (seeded splitmix64 on the GPU)",
         "config": {"workload": {
-            "ntt": "C2: batched forward+inverse negacyclic NTT, N=16384, 6 primes ~50 bit, "
+            "ntt": "batched forward+inverse negacyclic NTT, N=16384, 6 primes ~50 bit, "
                    "256 ciphertexts x 2 polynomials = 3072 limbs",
-            "keyswitch": "C3: keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
-            "gemm": "C4: share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64"}[key],
+            "keyswitch": "keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
+            "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64"}[key],
             "N": N, "parallelism": "single GPU"},
         "roofline": primary["roofline"],
         "cpu_baseline": cpu.get(key),

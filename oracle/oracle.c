@@ -13,7 +13,7 @@
  * absent here, so the SEAL conventions are restated from its published
  * algorithm (NTTTables, ntt_negacyclic_harvey, barrett_reduce_128,
  * RNSTool::divide_and_round_q_last, GaloisTool::apply_galois) and pinned by
- * closed-form tests (tests/test_oracle_*.py).
+ * closed-form tests (tests/test_oracle.py, tests/golden/closed_form.py).
  *
  * Every residue handed in or out is canonical ([0, q)).  q < 2^62 throughout.
  */

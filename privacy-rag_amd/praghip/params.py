@@ -49,16 +49,16 @@ def primes_below(bits: int, n: int, count: int) -> list[int]:
     return sorted(out)
 
 
-def c1_primes() -> list[int]:
+def primes_n4096_54bit() -> list[int]:
     """N=4096, two ~54-bit primes."""
     return primes_below(54, 4096, 2)
 
 
-def c2_primes() -> list[int]:
+def primes_n16384_50bit() -> list[int]:
     """N=16384, six ~50-bit primes."""
     return primes_below(50, 16384, 6)
 
 
-def c3_primes() -> list[int]:
+def primes_n16384_switch() -> list[int]:
     """N=16384: six ~50-bit data primes + one ~60-bit special prime (last)."""
     return primes_below(50, 16384, 6) + primes_below(60, 16384, 1)

@@ -68,7 +68,7 @@ def test_gemm_extreme_values(gpu):
 
 
 def test_gemm_c4_full_shape(gpu):
-    """C4: activation shares u64 [512 x 1024] times int8 [3072 x 1024] -> [512 x 3072] mod 2^64."""
+    """Qwen3 up/gate shape: activation shares u64 [512 x 1024] times int8 [3072 x 1024] -> [512 x 3072] mod 2^64."""
     m, k, n = 512, 1024, 3072
     x = oracle.fill_u64(m * k, 0x5052414700000004).reshape(m, k)
     w = oracle.fill_i8(n * k, 0x5052414700000104).reshape(n, k)

@@ -11,7 +11,7 @@ from conftest import from_dev, to_dev
 
 pytestmark = pytest.mark.gpu
 
-C3 = cf.primes_below(50, 16384, 6) + cf.primes_below(60, 16384, 1)
+P16384_SWITCH = cf.primes_below(50, 16384, 6) + cf.primes_below(60, 16384, 1)
 
 
 def test_keyswitch_golden_fixtures(gpu, golden_dir):
@@ -43,8 +43,8 @@ def test_keyswitch_locked_reference_dnum6(gpu, element):
 
 @pytest.mark.parametrize("dnum", [3, 2, 6])
 def test_keyswitch_c3_modup_per_ciphertext_keys(gpu, dnum):
-    """C3 shape: 6 data primes ~50 bits + 60-bit special prime, dnum digits, one key per ciphertext."""
-    q, n, L, batch = C3, 16384, 6, 3
+    """P16384_SWITCH shape: 6 data primes ~50 bits + 60-bit special prime, dnum digits, one key per ciphertext."""
+    q, n, L, batch = P16384_SWITCH, 16384, 6, 3
     print(f"[ks] c3 dnum={dnum}", flush=True)
     ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000303).reshape(batch, 2, L, n)
     keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x5052414700010303).reshape(
@@ -62,7 +62,7 @@ def test_keyswitch_c3_modup_per_ciphertext_keys(gpu, dnum):
 
 def test_keyswitch_edge_inputs(gpu):
     """Zero ciphertext, all q-1, and the check_switch.cpp:20 patterns in c1."""
-    q, n, L, dnum = C3, 16384, 6, 3
+    q, n, L, dnum = P16384_SWITCH, 16384, 6, 3
     key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 77).reshape(dnum, 2, L + 1, n)
     sw = praghip.Switch(q, 14, dnum, key=key, element=3)
     qs = np.array(q[:L], dtype=np.uint64)[:, None]

@@ -12,8 +12,8 @@ from conftest import from_dev, to_dev
 
 pytestmark = pytest.mark.gpu
 
-C1 = cf.primes_below(54, 4096, 2)
-C2 = cf.primes_below(50, 16384, 6)
+P4096_54 = cf.primes_below(54, 4096, 2)
+P16384_50 = cf.primes_below(50, 16384, 6)
 
 
 def _roundtrip_case(q, log_n, limbs, seed, gpu, patterns=True):
@@ -47,12 +47,12 @@ def test_ntt_locked_primes(gpu):
 
 
 def test_ntt_c2_primes_f64_path(gpu):
-    _roundtrip_case(C2, 14, 24, 0x5052414700000102, gpu)
+    _roundtrip_case(P16384_50, 14, 24, 0x5052414700000102, gpu)
 
 
 def test_ntt_c1_config(gpu):
-    # C1: N=4096, 2 primes ~54 bits, 16 polynomials x 2 limbs
-    _roundtrip_case(C1, 12, 32, 0x5052414700000001, gpu)
+    # N=4096, 2 primes ~54 bits, 16 polynomials x 2 limbs
+    _roundtrip_case(P4096_54, 12, 32, 0x5052414700000001, gpu)
 
 
 @pytest.mark.parametrize("log_n", [4, 5, 6, 7, 9, 11, 13])
@@ -94,11 +94,11 @@ def test_ntt_golden_sampled_full_size(gpu, golden_dir):
 
 
 def test_ntt_c2_full_batch_properties(gpu):
-    """C2 at full size: 256 ciphertexts x 2 x 6 primes = 3072 limbs.  Bit-exact
+    """P16384_50 at full size: 256 ciphertexts x 2 x 6 primes = 3072 limbs.  Bit-exact
     forward against the oracle on a slice, round trip and linearity on all."""
     import torch
     n, limbs = 16384, 3072
-    q = C2
+    q = P16384_50
     plan = praghip.NttBatch(q, 14)
     a = oracle.fill_residues(limbs, n, q, 0x5052414700000002)
     t = to_dev(a)
@@ -158,7 +158,7 @@ def test_ntt_host_api_and_errors(gpu):
 
 def test_ntt_rejects_misaligned_device_buffer(gpu):
     import torch
-    plan = praghip.NttBatch(C2, 14)
+    plan = praghip.NttBatch(P16384_50, 14)
     buf = torch.zeros(16384 + 1, dtype=torch.int64, device="cuda")
     with pytest.raises(praghip.PraghipError) as e:
         plan.forward(buf[1:])  # 8-byte aligned view

@@ -262,3 +262,20 @@ def test_lift_and_local_scale():
         m = sum(int(a) * int(b) for a, b in zip(shares[s], w)) % t
         want = [((Q * m + t // 2) // t) % x for x in q]  # round(Q*m/t) mod q_k
         assert got[s].tolist() == want
+
+
+def test_dyadic_mac_closed_form():
+    """out[l][z] = sum_b a[b][l][z] * w[b][l % wl][z] mod q[l % P], by Python integers,
+    with extreme residues (q-1) in block 0 so a dropped reduction shows."""
+    q = [cf.LOCKED_PRIMES[0], cf.LOCKED_PRIMES[5], cf.primes_below(50, 64, 1)[0]]
+    blocks, limbs, n = 5, 6, 32
+    a = oracle.fill_residues(blocks * limbs, n, q, 21).reshape(blocks, limbs, n)
+    w = oracle.fill_residues(blocks * 3, n, q, 22).reshape(blocks, 3, n)
+    for l in range(limbs):
+        a[0, l, :4] = q[l % 3] - 1
+        w[0, l % 3, :4] = q[l % 3] - 1
+    got = oracle.dyadic_mac(a, w, q)
+    for l in range(limbs):
+        ql = q[l % 3]
+        want = [sum(int(a[b, l, z]) * int(w[b, l % 3, z]) for b in range(blocks)) % ql for z in range(n)]
+        assert got[l].tolist() == want, l
