@@ -8,10 +8,12 @@
 // Barrett-128 for products of two runtime residues (switch.cu:30-45).
 //
 // Float path (q < 2^50): residues held as exact integers in IEEE doubles.  The
-// product a*w is split error-free into hi + lo with one FMA, the quotient is
-// rounded with the 1.5*2^52 shifter, and the remainder hi - c*q is exact
-// because it is an integer below 2^53.  Results are centred: |r| <= 0.76 q for
-// |a| <= 2q, w < q.
+// product a*w is split error-free into hi + lo with one FMA, the quotient
+// c = rint(a * fl(w * fl(1/q))) is within 1/2 + 3|a|/8q of a*w/q (three
+// roundings of relative size 2^-53, |a*w/q| < |a| < |a|/q * 2^50), and the
+// remainder hi - c*q is exact because it is an integer below 2^53.  Results
+// are centred: |r| <= (1/2 + 3A/8) q for |a| <= A q, w < q; any A <= 4 keeps
+// every intermediate below 2^53.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -69,22 +71,21 @@ PH_HD uint64_t mul_barrett(uint64_t a, uint64_t b, const Barrett m) {
 }
 
 // -------------------------------------------------------------------- float
-constexpr double kShifter = 6755399441055744.0;  // 1.5 * 2^52: x + S - S = rint(x) for |x| < 2^51
-
 struct ShoupF {
   double w, wq;  // operand (exact integer), operand / q
 };
 
-// a*w mod q, centred: |r| <= 0.76 q for |a| <= 2q (q < 2^50, w < q).
+// a*w mod q, centred: |r| <= (1/2 + 3A/8) q for |a| <= A q, A <= 4 (q < 2^50,
+// w < q, wq = w * (1/q)).
 PH_HD double mul_f64(double a, double w, double wq, double q) {
   const double hi = a * w;
   const double lo = __builtin_fma(a, w, -hi);
-  const double c = __builtin_fma(a, wq, kShifter) - kShifter;
+  const double c = __builtin_rint(a * wq);
   return __builtin_fma(-c, q, hi) + lo;
 }
-// x mod q, centred to |r| <= q/2 + 1 for |x| < 2^51 (qinv = 1/q).
+// x mod q, centred to |r| <= q/2 + 1 for |x| < 2^53 (qinv = 1/q).
 PH_HD double reduce_f64(double x, double q, double qinv) {
-  const double c = __builtin_fma(x, qinv, kShifter) - kShifter;
+  const double c = __builtin_rint(x * qinv);
   return __builtin_fma(-c, q, x);
 }
 // centred residue (|x| < 2q) -> canonical [0, q)

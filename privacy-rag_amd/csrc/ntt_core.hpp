@@ -21,7 +21,8 @@
 //   ArU64 - any q < 2^62: Harvey's lazy butterflies (forward values in [0,4q),
 //           inverse in [0,2q)) over Shoup twiddle pairs, canonical at the end;
 //   ArF64 - q < 2^50: residues as exact integers in doubles, products with an
-//           error-free FMA split, centred values re-centred every second stage.
+//           error-free FMA split, values re-centred every fourth forward /
+//           third inverse stage.
 // Both produce the canonical residue of the same transform, so the result is
 // bit-identical to the reference whatever the path.
 #pragma once
@@ -77,16 +78,21 @@ struct ArU64 {
     y = mul_shoup_lazy(d, p.last, p.last_q, q);
   }
   __device__ __forceinline__ void settle(T&) const {}
+  // Harvey's bounds hold without re-centring
+  static constexpr bool settle_fwd(int) { return false; }
+  static constexpr bool settle_inv(int) { return false; }
 };
 
-// Float path bounds (q < 2^50, so q * 2^-52 < 1/4).  For |a| <= B q the
-// quotient estimate c = rint(a * fl(w * fl(1/q))) is within 1/2 + B/4 of
-// a w / q, so |a w - c q| <= (1/2 + B/4) q, computed exactly (an integer
-// below 2^53 formed by FMAs from the error-free split of a w).
-//   forward : every value re-centred to <= q/2 + 1 each second stage; in
-//             between B <= 1.13 and outputs stay below 2.7 q;
-//   inverse : sums re-centred every stage, differences go through the
-//             product, so every value stays <= q.
+// Float path bounds (q < 2^50, |x| <= M q, mul_f64 gives |t| <= (1/2 + 3A/8) q
+// for a factor |a| <= A q, A <= 4; sums must stay below 2^53 = 8 * 2^50):
+//   forward : inputs |x| <= q; stages 0..2 grow the bound 1 -> 1.88 -> 3.08
+//             -> 4.73, every value is re-centred (|x| <= q/2 + 1) after
+//             stages s = 2 mod 4, and four stages from there reach 1.19,
+//             2.14, 3.44, 5.23 - factors stay below 3.5 q;
+//   inverse : the sum side doubles and the difference goes through the
+//             product: from |x| <= q, 2 -> 4 after stages 0, 1; re-centred after
+//             stages l = 1 mod 3, then 1 -> 2 -> 4 (differences below 4 q);
+//             the last stage multiplies both outputs (N^-1 folded).
 struct ArF64 {
   using T = double;
   using TW = double;  // w; w/q is formed in registers
@@ -114,7 +120,7 @@ struct ArF64 {
   }
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
     const T s = x + y, d = x - y;
-    x = reduce_f64(s, q, qinv);
+    x = s;
     y = mul(d, w);
   }
   __device__ __forceinline__ void inv_last(T& x, T& y, const NttPrime& p) const {
@@ -123,6 +129,8 @@ struct ArF64 {
     y = mul(d, p.last_f);
   }
   __device__ __forceinline__ void settle(T& x) const { x = reduce_f64(x, q, qinv); }
+  static constexpr bool settle_fwd(int s) { return s % 4 == 2; }
+  static constexpr bool settle_inv(int l) { return l % 3 == 1; }
 };
 
 // Pass geometry.  Forward passes take 4 gap bits from the top down, the last
@@ -272,7 +280,7 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename 
           ar.fwd(v[j0], v[j1], w[n]);
         }
       }
-      if ((s & 1) && s != LOGN - 1) {  // the final stage is reduced on output
+      if (A::settle_fwd(s) && s != LOGN - 1) {  // the final stage is reduced on output
 #pragma unroll
         for (int m = 0; m < (1 << R); ++m) ar.settle(v[(b << R) | m]);
       }
@@ -302,6 +310,10 @@ __device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename 
           else
             ar.inv(v[j0], v[j1], w[n]);
         }
+      }
+      if (A::settle_inv(l) && l != LOGN - 1) {
+#pragma unroll
+        for (int m = 0; m < (1 << R); ++m) ar.settle(v[(b << R) | m]);
       }
       if (is_mid<R>(b, i)) mid();
     }
