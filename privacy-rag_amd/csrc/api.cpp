@@ -529,7 +529,8 @@ struct praghip_switch_plan {
   NttDevice d;
   KsConst kc{};
   KsConst* kc_dev = nullptr;
-  uint64_t *key = nullptr, *expanded = nullptr, *prod = nullptr, *in = nullptr, *out = nullptr;
+  uint64_t *key = nullptr, *acc = nullptr, *prod = nullptr, *in = nullptr, *out = nullptr;
+  unsigned acc_slots = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev[4] = {};
   praghip_timing timing{};
@@ -634,7 +635,10 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
   if (e == hipSuccess) e = hipMemcpyAsync(p->kc_dev, &p->kc, sizeof(KsConst), hipMemcpyHostToDevice, p->stream);
   if (e == hipSuccess && key) e = p->buf.alloc((void**)&p->key, key_words * 8, true);
   if (e == hipSuccess && key) e = hipMemcpyAsync(p->key, key, key_words * 8, hipMemcpyHostToDevice, p->stream);
-  if (e == hipSuccess) e = p->buf.alloc((void**)&p->expanded, max_batch * dnum * K * n * 8, true);
+  if (e == hipSuccess) {
+    p->acc_slots = ks_acc_slots(int(log_n));
+    e = p->acc_slots ? p->buf.alloc((void**)&p->acc, size_t(p->acc_slots) * 2 * n * 8, true) : hipErrorInvalidValue;
+  }
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, max_batch * 2 * K * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->in, 2 * L * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->out, 2 * L * n * 8, true);
@@ -656,7 +660,8 @@ static hipError_t keyswitch_chunks(praghip_switch_plan* p, const uint64_t* in, u
     a.out = out + b0 * ct_words;
     a.key = keys + b0 * key_stride;
     a.key_stride = key_stride;
-    a.expanded = p->expanded;
+    a.acc = p->acc;
+    a.acc_slots = p->acc_slots;
     a.prod = p->prod;
     a.galois_inv = ginv;
     const hipError_t e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);

@@ -50,8 +50,9 @@ struct KsArgs {
   uint64_t* out;         // [batch][2][L][N]
   const uint64_t* key;   // [dnum][2][K][N] NTT form, + b * key_stride
   size_t key_stride;     // words between consecutive ciphertexts' keys (0 = shared)
-  uint64_t* expanded;    // scratch [batch][dnum][K][N]
-  uint64_t* prod;        // scratch [batch][2][K][N]
+  uint64_t* acc;         // scratch [acc_slots][2][N]: per-workgroup running sums
+  unsigned acc_slots;
+  uint64_t* prod;        // scratch [batch][2][K][N]: products in coefficient form
   size_t batch;
   uint32_t galois_inv;   // g^-1 mod 2N (1 = identity)
 };
@@ -68,5 +69,8 @@ hipError_t launch_fill_i8(int8_t* out, size_t count, uint64_t seed, hipStream_t 
 
 hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
                             hipStream_t s);
+// Workgroups of the fused keyswitch kernel for 2^log_n (the acc slots a plan
+// allocates); 0 for an unsupported size.
+unsigned ks_acc_slots(int log_n);
 
 }  // namespace praghip

@@ -12,92 +12,18 @@
 // The Galois automorphism a(X) -> a(X^g) is applied as a gather when c1 and
 // c0 are read: output coefficient k comes from i = k * g^-1 mod 2N, negated
 // when i >= N.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace praghip {
 
 __device__ __forceinline__ uint64_t galois_read(const uint64_t* __restrict__ limb, unsigned k, uint32_t ginv,
                                                 int log_n, uint64_t q) {
-  if (ginv == 1) return limb[k];
-  const unsigned two_n_mask = (2u << log_n) - 1;
-  const unsigned i = (unsigned)(((uint64_t)k * ginv) & two_n_mask);
+  // branch-free: ginv = 1 gives i = k and no negation
+  const unsigned i = (k * ginv) & ((2u << log_n) - 1);
   const uint64_t v = limb[i & ((1u << log_n) - 1)];
   return ((i >> log_n) && v) ? q - v : v;
-}
-
-// One thread per (ciphertext, coefficient): reads the c1 residues once and
-// writes every (digit, key prime) value of that coefficient.
-__global__ void __launch_bounds__(256)
-    ks_modup_kernel(const uint64_t* __restrict__ in, uint64_t* __restrict__ expanded,
-                    const KsConst* __restrict__ kcp, size_t batch, uint32_t ginv) {
-  const KsConst& kc = *kcp;
-  const int L = kc.L, K = kc.K, log_n = kc.log_n;
-  const size_t n = size_t(1) << log_n;
-  const size_t total = batch * n;
-  for (size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += size_t(gridDim.x) * blockDim.x) {
-    const size_t b = idx >> log_n;
-    const unsigned k = unsigned(idx & (n - 1));
-    const uint64_t* c1 = in + (b * 2 + 1) * L * n;
-    uint64_t v[kMaxKeyPrimes];
-#pragma unroll
-    for (int i = 0; i < kMaxKeyPrimes; ++i)
-      if (i < L) v[i] = galois_read(c1 + i * n, k, ginv, log_n, kc.q[i]);
-    uint64_t* eb = expanded + b * size_t(kc.dnum) * K * n;
-    for (int j = 0; j < kc.dnum; ++j) {
-      const int lo = kc.dig_lo[j], hi = kc.dig_lo[j + 1];
-      uint64_t y[kMaxKeyPrimes];
-#pragma unroll
-      for (int i = 0; i < kMaxKeyPrimes; ++i)
-        if (i >= lo && i < hi) y[i] = mul_shoup(v[i], kc.inv_hat[i].w, kc.inv_hat[i].wq, kc.q[i]);
-      for (int t = 0; t < K; ++t) {
-        uint64_t e;
-        if (t >= lo && t < hi) {
-          e = v[t];
-        } else {
-          const uint64_t qt = kc.q[t], qt2 = 2 * qt;
-          uint64_t acc = 0;
-#pragma unroll
-          for (int i = 0; i < kMaxKeyPrimes; ++i)
-            if (i >= lo && i < hi) {
-              acc += mul_shoup_lazy(y[i], kc.hat[i][t].w, kc.hat[i][t].wq, qt);  // [0, 2q_t)
-              acc = acc >= qt2 ? acc - qt2 : acc;
-            }
-          e = acc >= qt ? acc - qt : acc;
-        }
-        eb[(size_t(j) * K + t) * n + k] = e;
-      }
-    }
-  }
-}
-
-// One thread per (ciphertext, key prime, coefficient): both components.
-__global__ void __launch_bounds__(256)
-    ks_product_kernel(const uint64_t* __restrict__ expanded, const uint64_t* __restrict__ key, size_t key_stride,
-                      uint64_t* __restrict__ prod, const KsConst* __restrict__ kcp, size_t batch) {
-  const KsConst& kc = *kcp;
-  const int K = kc.K, dnum = kc.dnum, log_n = kc.log_n;
-  const size_t n = size_t(1) << log_n;
-  const size_t total = batch * K * n;
-  for (size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += size_t(gridDim.x) * blockDim.x) {
-    const size_t k = idx & (n - 1);
-    const size_t bt = idx >> log_n;
-    const int t = int(bt % unsigned(K));
-    const size_t b = bt / unsigned(K);
-    const Barrett m = kc.bar[t];
-    const uint64_t* e = expanded + b * size_t(dnum) * K * n + size_t(t) * n + k;
-    const uint64_t* kb = key + b * key_stride + size_t(t) * n + k;
-    uint64_t s0 = 0, s1 = 0;
-    for (int j = 0; j < dnum; ++j) {
-      const uint64_t x = e[size_t(j) * K * n];
-      s0 = add_mod(s0, mul_barrett(x, kb[(size_t(j) * 2 + 0) * K * n], m), m.q);
-      s1 = add_mod(s1, mul_barrett(x, kb[(size_t(j) * 2 + 1) * K * n], m), m.q);
-    }
-    uint64_t* pb = prod + b * 2 * K * n + size_t(t) * n + k;
-    pb[0] = s0;
-    pb[size_t(K) * n] = s1;
-  }
 }
 
 // One thread per (ciphertext, coefficient): ModDown of both components.
@@ -129,23 +55,312 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// ------------------------------------------------------------------ fused
+// One workgroup per (ciphertext b, key prime t): ModUp of every digit to prime
+// t, its forward NTT, the key inner product and the inverse NTT of both
+// product components, with the limb held in registers + LDS throughout.  The
+// coefficient-form products go to `prod` for ModDown.  Per digit the two
+// running sums live in a per-workgroup slot in global memory, in a
+// thread-private layout (register r of thread th at [c][r][th]): coalesced,
+// and re-read by the same workgroup shortly after, so they stay in cache.
+//
+// Arithmetic per prime: the float path when every data prime and t are below
+// 2^50 (ModUp, product and transforms in exact FP64), otherwise the integer
+// path (Shoup ModUp, Barrett-128 products as in switch.cu:30-45, Harvey
+// transforms).  The special prime (60 bits) takes the integer path.
+struct KsFused {
+  const uint64_t* in;      // [batch][2][L][N]
+  const uint64_t* key;     // [dnum][2][K][N] per ciphertext, key_stride words apart
+  size_t key_stride;
+  uint64_t* prod;          // [batch][2][K][N] coefficient form
+  uint64_t* acc;           // [gridDim.x][2][N] running sums
+  const KsConst* kc;
+  const NttPrime* primes;  // [K]
+  const ulonglong2* tw_fwd_u;
+  const ulonglong2* tw_inv_u;
+  const double* tw_fwd_f;
+  const double* tw_inv_f;
+  unsigned batch, items;
+  unsigned acc_slots;  // workgroups the acc buffer has room for
+  uint32_t ginv;
+  int data_f64;  // every data prime is below 2^50
+  int xcd;       // items of one ciphertext on one XCD (batch and grid multiples of 8)
+};
+
+__device__ __forceinline__ uint64_t as_u64(double x) { return (uint64_t)__double_as_longlong(x); }
+__device__ __forceinline__ double as_f64(uint64_t x) { return __longlong_as_double((long long)x); }
+
+// ModUp of digit j to prime t for this thread's registers (forward-input
+// layout): e[r] = c1_t when t is one of the digit's primes, else
+// sum_i [c1_i (Q_j/q_i)^-1]_{q_i} (Q_j/q_i) mod q_t over the digit's primes
+// (fast base conversion, no correction).  The per-prime constants are read
+// once per digit prime, outside the loop over registers.
+template <int LOGN>
+__device__ __forceinline__ void modup_f64(double (&e)[kE], const KsFused& f, const KsConst& kc, const uint64_t* c1,
+                                          int j, int t, const NttPrime& pt, unsigned th) {
+  const int lo = kc.dig_lo[j], hi = kc.dig_lo[j + 1];
+  if (t >= lo && t < hi) {
+    const uint64_t* x = c1 + (size_t(t) << LOGN);
+    const uint64_t q = kc.q[t];
+#pragma unroll
+    for (int r = 0; r < kE; ++r) e[r] = ArF64::from_u64(galois_read(x, fwd_in_index<LOGN>(th, r), f.ginv, LOGN, q));
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < kE; ++r) e[r] = 0.0;
+  for (int i = lo, n = 0; i < hi; ++i, ++n) {
+    const NttPrime pi = f.primes[i];
+    const uint64_t* x = c1 + (size_t(i) << LOGN);
+    const double ih = double(kc.inv_hat[i].w), ihq = ih * pi.qinv;
+    const double hf = double(kc.hat[i][t].w), hfq = hf * pt.qinv;
+    const uint64_t qi = kc.q[i];
+#pragma unroll
+    for (int r = 0; r < kE; ++r) {
+      const double v = ArF64::from_u64(galois_read(x, fwd_in_index<LOGN>(th, r), f.ginv, LOGN, qi));
+      const double y = canon_f64(mul_f64(v, ih, ihq, pi.qd), pi.qd);  // [x (Q_j/q_i)^-1]_{q_i}
+      e[r] += mul_f64(y, hf, hfq, pt.qd);                             // |term| < 7q/8
+    }
+    if ((n & 3) == 3) {
+#pragma unroll
+      for (int r = 0; r < kE; ++r) e[r] = reduce_f64(e[r], pt.qd, pt.qinv);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kE; ++r) e[r] = reduce_f64(e[r], pt.qd, pt.qinv);
+}
+template <int LOGN>
+__device__ __forceinline__ void modup_u64(uint64_t (&e)[kE], const KsFused& f, const KsConst& kc, const uint64_t* c1,
+                                          int j, int t, unsigned th) {
+  const int lo = kc.dig_lo[j], hi = kc.dig_lo[j + 1];
+  const uint64_t qt = kc.q[t], qt2 = 2 * qt;
+  if (t >= lo && t < hi) {
+    const uint64_t* x = c1 + (size_t(t) << LOGN);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) e[r] = galois_read(x, fwd_in_index<LOGN>(th, r), f.ginv, LOGN, qt);
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < kE; ++r) e[r] = 0;
+  for (int i = lo; i < hi; ++i) {
+    const uint64_t* x = c1 + (size_t(i) << LOGN);
+    const Shoup ih = kc.inv_hat[i], hf = kc.hat[i][t];
+    const uint64_t qi = kc.q[i];
+#pragma unroll
+    for (int r = 0; r < kE; ++r) {
+      const uint64_t y = mul_shoup(galois_read(x, fwd_in_index<LOGN>(th, r), f.ginv, LOGN, qi), ih.w, ih.wq, qi);
+      const uint64_t a = e[r] + mul_shoup_lazy(y, hf.w, hf.wq, qt);  // [0, 4q_t)
+      e[r] = a >= qt2 ? a - qt2 : a;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kE; ++r) e[r] = e[r] >= qt ? e[r] - qt : e[r];
+}
+
+// Float path item.  acc0 stays in registers; component 1's running sum goes
+// through the workgroup's slot.
+template <int LOGN>
+__device__ __forceinline__ void ks_item_f64(const KsFused& f, const KsConst& kc, unsigned b, int t, uint64_t* lds,
+                                            uint64_t* slot) {
+  using A = ArF64Lean;
+  constexpr unsigned TH = ntt_threads<LOGN>();
+  const NttPrime pr = f.primes[t];
+  const A ar(pr);
+  const int K = kc.K, L = kc.L, dnum = kc.dnum;
+  const uint64_t* c1 = f.in + (((size_t(b) * 2 + 1) * size_t(L)) << LOGN);
+  const uint64_t* kb = f.key + size_t(b) * f.key_stride + (size_t(t) << LOGN);
+  double* xl = reinterpret_cast<double*>(lds);
+  uint64_t* s1 = slot;
+  double acc0[kE];
+  for (int j = 0; j < dnum; ++j) {
+    // thread index made loop-variant (j < 2^30): per-thread indices are
+    // recomputed per digit instead of being hoisted and kept live (or
+    // spilled) across the transforms
+    const unsigned th = threadIdx.x + (unsigned(j) >> 30);
+    double e[kE];
+    modup_f64<LOGN>(e, f, kc, c1, j, t, pr, th);
+    ntt_regs<LOGN, false>(e, xl, th, f.tw_fwd_f + (size_t(t) << LOGN), ar, pr);
+    const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << LOGN);
+    const uint64_t* k1 = k0 + (size_t(K) << LOGN);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) {
+      const unsigned pos = fwd_out_index<LOGN>(th, r), si = unsigned(r) * TH + th;
+      // |e| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
+      const double p0 = ar.mul(e[r], ArF64::from_u64(k0[pos]));
+      double p1 = ar.mul(e[r], ArF64::from_u64(k1[pos]));
+      acc0[r] = reduce_f64(j ? acc0[r] + p0 : p0, ar.q, ar.qinv);
+      if (j) p1 += as_f64(s1[si]);
+      s1[si] = as_u64(reduce_f64(p1, ar.q, ar.qinv));
+      if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << LOGN);
+  {
+    const unsigned th = threadIdx.x + (unsigned(dnum) >> 30);
+    ntt_regs<LOGN, true>(acc0, xl, th, f.tw_inv_f + (size_t(t) << LOGN), ar, pr);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) pb[inv_out_index<LOGN>(th, r)] = ar.to_u64_inv(acc0[r]);
+  }
+  {
+    const unsigned th = threadIdx.x + (unsigned(dnum + 1) >> 30);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) acc0[r] = as_f64(s1[unsigned(r) * TH + th]);
+    ntt_regs<LOGN, true>(acc0, xl, th, f.tw_inv_f + (size_t(t) << LOGN), ar, pr);
+    uint64_t* pc = pb + (size_t(K) << LOGN);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) pc[inv_out_index<LOGN>(th, r)] = ar.to_u64_inv(acc0[r]);
+  }
+}
+
+// Integer path item (special prime, primes of 50 bits or more): both running
+// sums go through the workgroup's slot.
+template <int LOGN>
+__device__ __forceinline__ void ks_item_u64(const KsFused& f, const KsConst& kc, unsigned b, int t, uint64_t* lds,
+                                            uint64_t* slot) {
+  using A = ArU64;
+  constexpr unsigned TH = ntt_threads<LOGN>();
+  const NttPrime pr = f.primes[t];
+  const A ar(pr);
+  const int K = kc.K, L = kc.L, dnum = kc.dnum;
+  const uint64_t* c1 = f.in + (((size_t(b) * 2 + 1) * size_t(L)) << LOGN);
+  const uint64_t* kb = f.key + size_t(b) * f.key_stride + (size_t(t) << LOGN);
+  uint64_t* s0 = slot;
+  uint64_t* s1 = slot + (size_t(kE) * TH);
+  const Barrett bar = kc.bar[t];
+  for (int j = 0; j < dnum; ++j) {
+    const unsigned th = threadIdx.x + (unsigned(j) >> 30);
+    uint64_t e[kE];
+    modup_u64<LOGN>(e, f, kc, c1, j, t, th);
+    ntt_regs<LOGN, false>(e, lds, th, f.tw_fwd_u + (size_t(t) << LOGN), ar, pr);
+    const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << LOGN);
+    const uint64_t* k1 = k0 + (size_t(K) << LOGN);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) {
+      const unsigned pos = fwd_out_index<LOGN>(th, r), si = unsigned(r) * TH + th;
+      const uint64_t x = ar.to_u64_fwd(e[r]);
+      uint64_t p0 = mul_barrett(x, k0[pos], bar);
+      uint64_t p1 = mul_barrett(x, k1[pos], bar);
+      if (j) {
+        p0 = add_mod(p0, s0[si], pr.q);
+        p1 = add_mod(p1, s1[si], pr.q);
+      }
+      s0[si] = p0;
+      s1[si] = p1;
+      if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << LOGN);
+#pragma unroll 1
+  for (int c = 0; c < 2; ++c) {
+    const unsigned th = threadIdx.x + (unsigned(c + dnum) >> 30);
+    const uint64_t* sc = c ? s1 : s0;
+    uint64_t e[kE];
+#pragma unroll
+    for (int r = 0; r < kE; ++r) e[r] = sc[unsigned(r) * TH + th];
+    ntt_regs<LOGN, true>(e, lds, th, f.tw_inv_u + (size_t(t) << LOGN), ar, pr);
+    uint64_t* pc = pb + ((size_t(c) * K) << LOGN);
+#pragma unroll
+    for (int r = 0; r < kE; ++r) pc[inv_out_index<LOGN>(th, r)] = ar.to_u64_inv(e[r]);
+  }
+}
+
+template <int LOGN>
+__global__ void __launch_bounds__(ntt_threads<LOGN>()) ks_fused_kernel(KsFused f) {
+  __shared__ __attribute__((aligned(16))) uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
+  const KsConst& kc = *f.kc;
+  const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
+  uint64_t* slot = f.acc + (size_t(blockIdx.x) * 2 * kE * ntt_threads<LOGN>());
+  for (unsigned v = blockIdx.x; v < f.items; v += gridDim.x) {
+    unsigned b, t;
+    if (f.xcd) {  // item v runs on XCD v % 8: keep a ciphertext's K items there
+      const unsigned u = v >> 3;
+      b = (v & 7) + 8 * (u / K);
+      t = u % K;
+    } else {
+      b = v / K;
+      t = v % K;
+    }
+    __syncthreads();  // the previous item's LDS use is over
+    if (f.data_f64 && t < L)
+      ks_item_f64<LOGN>(f, kc, b, int(t), lds, slot);
+    else
+      ks_item_u64<LOGN>(f, kc, b, int(t), lds, slot);
+  }
+}
+
 static unsigned grid_for(size_t work) { return unsigned(std::min<size_t>((work + 255) / 256, 1u << 20)); }
+
+template <int LOGN>
+static unsigned fused_grid() {
+  static unsigned grid = 0;
+  if (!grid) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ks_fused_kernel<LOGN>, ntt_threads<LOGN>(), 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    grid = unsigned(cus * per_cu);
+  }
+  return grid;
+}
+
+#define PH_LOGN_SWITCH(EXPR)      \
+  switch (log_n) {                \
+    case 4: { constexpr int LG = 4; EXPR; } \
+    case 5: { constexpr int LG = 5; EXPR; } \
+    case 6: { constexpr int LG = 6; EXPR; } \
+    case 7: { constexpr int LG = 7; EXPR; } \
+    case 8: { constexpr int LG = 8; EXPR; } \
+    case 9: { constexpr int LG = 9; EXPR; } \
+    case 10: { constexpr int LG = 10; EXPR; } \
+    case 11: { constexpr int LG = 11; EXPR; } \
+    case 12: { constexpr int LG = 12; EXPR; } \
+    case 13: { constexpr int LG = 13; EXPR; } \
+    case 14: { constexpr int LG = 14; EXPR; } \
+    default: break;               \
+  }
+
+unsigned ks_acc_slots(int log_n) {
+  PH_LOGN_SWITCH(return fused_grid<LG>());
+  return 0;
+}
+
+template <int LOGN>
+static hipError_t launch_fused_n(KsFused f, hipStream_t s) {
+  const unsigned blocks = std::min(f.items, std::min(fused_grid<LOGN>(), f.acc_slots));
+  f.xcd = (f.batch % 8 == 0 && blocks % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((ks_fused_kernel<LOGN>), dim3(blocks), dim3(ntt_threads<LOGN>()), 0, s, f);
+  return hipGetLastError();
+}
 
 hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
                             hipStream_t s) {
   if (a.batch == 0) return hipSuccess;
   const size_t n = size_t(1) << kc.log_n;
-  hipLaunchKernelGGL(ks_modup_kernel, dim3(grid_for(a.batch * n)), dim3(256), 0, s, a.in, a.expanded, kc_dev,
-                     a.batch, a.galois_inv);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  e = launch_ntt(false, a.expanded, a.batch * kc.dnum * kc.K, d, s);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(ks_product_kernel, dim3(grid_for(a.batch * kc.K * n)), dim3(256), 0, s, a.expanded, a.key,
-                     a.key_stride, a.prod, kc_dev, a.batch);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  e = launch_ntt(true, a.prod, a.batch * 2 * kc.K, d, s);
+  KsFused f;
+  f.in = a.in;
+  f.key = a.key;
+  f.key_stride = a.key_stride;
+  f.prod = a.prod;
+  f.acc = a.acc;
+  f.kc = kc_dev;
+  f.primes = d.primes;
+  f.tw_fwd_u = d.tw_fwd_u;
+  f.tw_inv_u = d.tw_inv_u;
+  f.tw_fwd_f = d.tw_fwd_f;
+  f.tw_inv_f = d.tw_inv_f;
+  f.batch = unsigned(a.batch);
+  f.items = unsigned(a.batch * kc.K);
+  f.acc_slots = a.acc_slots;
+  f.ginv = a.galois_inv;
+  f.data_f64 = 1;
+  for (int i = 0; i < kc.L; ++i) f.data_f64 &= kc.q[i] < (1ull << 50) ? 1 : 0;
+  f.xcd = 0;
+  hipError_t e = hipErrorInvalidValue;
+  const int log_n = kc.log_n;
+  PH_LOGN_SWITCH(e = launch_fused_n<LG>(f, s); break);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(ks_moddown_kernel, dim3(grid_for(a.batch * n)), dim3(256), 0, s, a.prod, a.in, a.out, kc_dev,
                      a.batch, a.galois_inv);

@@ -101,7 +101,7 @@ struct ArF64 {
   __device__ explicit ArF64(const NttPrime& p) : q(p.qd), qinv(p.qinv) {}
   // Exact conversions for integers below 2^52: the bit pattern of 2^52 + x is
   // 0x4330... with x in its 52 mantissa bits.
-  __device__ __forceinline__ T from_u64(uint64_t x) const {
+  __device__ __forceinline__ static T from_u64(uint64_t x) {
     return __longlong_as_double((long long)(x | 0x4330000000000000ull)) - 4503599627370496.0;
   }
   __device__ __forceinline__ uint64_t to_u64(T x) const {
@@ -131,6 +131,13 @@ struct ArF64 {
   __device__ __forceinline__ void settle(T& x) const { x = reduce_f64(x, q, qinv); }
   static constexpr bool settle_fwd(int s) { return s % 4 == 2; }
   static constexpr bool settle_inv(int l) { return l % 3 == 1; }
+};
+
+// The float path with each pass's twiddles loaded when the pass starts (for
+// kernels that keep more than the limb in registers).
+struct ArF64Lean : ArF64 {
+  static constexpr bool kAhead = false;
+  __device__ explicit ArF64Lean(const NttPrime& p) : ArF64(p) {}
 };
 
 // Pass geometry.  Forward passes take 4 gap bits from the top down, the last
