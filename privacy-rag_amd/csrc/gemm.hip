@@ -56,8 +56,64 @@ __device__ __forceinline__ int weight_digit(int w, int e) {
   return (int)(int8_t)(w & 0xff);
 }
 
+// Global tile of one K step held in registers: the share loader's 8 u64 and
+// the weight loader's 32 weight bytes (as 8 words).
+struct TileRegs {
+  uint64_t xs[8];
+  uint32_t wb[8];
+};
+
 template <int WB>
-__global__ void __launch_bounds__(kThreads)
+__device__ __forceinline__ void load_tile(TileRegs& tr, const uint64_t* __restrict__ xrow, bool x_row_ok,
+                                          const void* __restrict__ wv, size_t wrow_off, bool w_row_ok, int k0, int K,
+                                          int ak, int wk, int wdigit, int w_vec) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int kk = k0 + ak + e;
+    tr.xs[e] = (x_row_ok && kk < K) ? xrow[kk] : 0;
+  }
+  const int kk = k0 + wk;
+  if (WB == 8) {
+    const int8_t* wrow = static_cast<const int8_t*>(wv) + wrow_off;
+    if (w_row_ok && kk + 32 <= K && w_vec) {
+      const uint4 a = *reinterpret_cast<const uint4*>(wrow + kk);
+      const uint4 b = *reinterpret_cast<const uint4*>(wrow + kk + 16);
+      tr.wb[0] = a.x; tr.wb[1] = a.y; tr.wb[2] = a.z; tr.wb[3] = a.w;
+      tr.wb[4] = b.x; tr.wb[5] = b.y; tr.wb[6] = b.z; tr.wb[7] = b.w;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const int kq = kk + 4 * q + bb;
+          const uint32_t byte = (w_row_ok && kq < K) ? uint8_t(wrow[kq]) : 0u;
+          word |= byte << (8 * bb);
+        }
+        tr.wb[q] = word;
+      }
+    }
+  } else {
+    const int32_t* wrow = static_cast<const int32_t*>(wv) + wrow_off;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        const int kq = kk + 4 * q + bb;
+        const int wvv = (w_row_ok && kq < K) ? wrow[kq] : 0;
+        word |= uint32_t(uint8_t(weight_digit(wvv, wdigit))) << (8 * bb);
+      }
+      tr.wb[q] = word;
+    }
+  }
+}
+
+// Two workgroups per CU (two waves per SIMD, accumulators in VGPRs): while
+// one waits on memory the other runs MFMAs.  Within a workgroup the next K
+// step's global loads are issued before the current step's MFMAs.
+template <int WB>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
     share_gemm_kernel(const uint64_t* __restrict__ x, const void* __restrict__ wv, const int8_t* __restrict__ shifts,
                       uint64_t* __restrict__ y, int M, int K, int N, uint64_t mask, int wdigit, int accumulate,
                       int w_vec) {
@@ -89,16 +145,17 @@ __global__ void __launch_bounds__(kThreads)
   const bool x_row_ok = (m0 + ar) < M;
   const bool w_row_ok = (n0 + wr) < N;
   const uint64_t* xrow = x + size_t(m0 + ar) * K;
+  const size_t wrow_off = size_t(n0 + wr) * K;
 
+  TileRegs tr;
+  load_tile<WB>(tr, xrow, x_row_ok, wv, wrow_off, w_row_ok, 0, K, ak, wk, wdigit, w_vec);
   for (int k0 = 0; k0 < K; k0 += kBK) {
     // ---- shares -> 8 offset-binary digit planes
     uint32_t d[16];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int kk = k0 + ak + e;
-      const uint64_t v = (x_row_ok && kk < K) ? xrow[kk] : 0;
-      d[2 * e] = uint32_t(v) ^ 0x80808080u;
-      d[2 * e + 1] = uint32_t(v >> 32) ^ 0x80808080u;
+      d[2 * e] = uint32_t(tr.xs[e]) ^ 0x80808080u;
+      d[2 * e + 1] = uint32_t(tr.xs[e] >> 32) ^ 0x80808080u;
     }
     uint32_t o[4][4];
     transpose4(d[0], d[2], d[4], d[6], o[0][0], o[0][1], o[0][2], o[0][3]);      // digits 0-3, k 0-3
@@ -111,48 +168,13 @@ __global__ void __launch_bounds__(kThreads)
       *reinterpret_cast<uint2*>(&a_lds[dg + 4][ar][ak]) = make_uint2(o[2][dg], o[3][dg]);
     }
     // ---- weights (digit `wdigit` of each) -> int8 rows
-    uint32_t wb[8];
-    if (WB == 8) {
-      const int8_t* wrow = static_cast<const int8_t*>(wv) + size_t(n0 + wr) * K;
-      const int kk = k0 + wk;
-      if (w_row_ok && kk + 32 <= K && w_vec) {
-        const uint4 a = *reinterpret_cast<const uint4*>(wrow + kk);
-        const uint4 b = *reinterpret_cast<const uint4*>(wrow + kk + 16);
-        wb[0] = a.x; wb[1] = a.y; wb[2] = a.z; wb[3] = a.w;
-        wb[4] = b.x; wb[5] = b.y; wb[6] = b.z; wb[7] = b.w;
-      } else {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          uint32_t word = 0;
-#pragma unroll
-          for (int bb = 0; bb < 4; ++bb) {
-            const int kq = kk + 4 * q + bb;
-            const uint32_t byte = (w_row_ok && kq < K) ? uint8_t(wrow[kq]) : 0u;
-            word |= byte << (8 * bb);
-          }
-          wb[q] = word;
-        }
-      }
-    } else {
-      const int32_t* wrow = static_cast<const int32_t*>(wv) + size_t(n0 + wr) * K;
-      const int kk = k0 + wk;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-          const int kq = kk + 4 * q + bb;
-          const int wvv = (w_row_ok && kq < K) ? wrow[kq] : 0;
-          word |= uint32_t(uint8_t(weight_digit(wvv, wdigit))) << (8 * bb);
-        }
-        wb[q] = word;
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) colsum = __builtin_amdgcn_sdot4(int(wb[q]), 0x01010101, colsum, false);
-    *reinterpret_cast<uint4*>(&w_lds[wr][wk]) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
-    *reinterpret_cast<uint4*>(&w_lds[wr][wk + 16]) = make_uint4(wb[4], wb[5], wb[6], wb[7]);
+    for (int q = 0; q < 8; ++q) colsum = __builtin_amdgcn_sdot4(int(tr.wb[q]), 0x01010101, colsum, false);
+    *reinterpret_cast<uint4*>(&w_lds[wr][wk]) = make_uint4(tr.wb[0], tr.wb[1], tr.wb[2], tr.wb[3]);
+    *reinterpret_cast<uint4*>(&w_lds[wr][wk + 16]) = make_uint4(tr.wb[4], tr.wb[5], tr.wb[6], tr.wb[7]);
     __syncthreads();
+    // ---- next step's loads, in flight during the MFMAs
+    if (k0 + kBK < K) load_tile<WB>(tr, xrow, x_row_ok, wv, wrow_off, w_row_ok, k0 + kBK, K, ak, wk, wdigit, w_vec);
 
     // ---- MFMA over the two 32-wide K steps
 #pragma unroll
