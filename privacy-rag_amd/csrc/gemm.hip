@@ -224,6 +224,192 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
+// ---------------------------------------------------------------- DMA path
+// For K % 64 == 0 and int8 weights (16-byte aligned x, w): the raw tiles go
+// from global memory straight into a two-stage LDS ring with
+// global_load_lds_dwordx4 (no registers, no wait until the stage is used), so
+// the next K step's loads are in flight during the current step's MFMAs; two
+// workgroups per CU overlap each other's waits as well.  Per step each thread
+// turns 8 shares of the raw tile into the 8 digit planes (as above), and the
+// weight tile is read by the MFMAs in place.
+//
+// LDS: raw shares [2][32 rows][512 B], weights [2][128 rows][64 B] with the
+// 16-byte chunk index of row r stored at chunk ^ (r & 3) (conflict-free
+// operand reads without padding, which DMA cannot insert), digit planes
+// [8][32][80 B].
+constexpr int kRawRow = kBK * 8;  // bytes of one raw share row per step
+
+// 16 bytes per lane from global memory straight into LDS at M0 + lane * 16
+// (global_load_lds_dwordx4).  Issued from inline asm, so the compiler adds no
+// wait of its own for it: the caller waits with s_waitcnt vmcnt(0) before any
+// wave reads what was loaded.
+__device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
+  const unsigned lds = unsigned(reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)(lds_wave_base)));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(src)
+               : "memory", "m0");
+}
+
+// One K step of the DMA path on stage buffers (raw, wt); the next step's DMAs
+// go to (raw_n, wt_n).  Distinct __shared__ objects per stage let the
+// compiler see that this step's LDS reads do not depend on the DMAs just
+// issued into the other stage (it would otherwise wait for them).
+struct DmaCtx {
+  const uint8_t* xsrc[4];
+  const int8_t* wsrc[2];
+  int wave, ar, ak, cl, ch, i, khalf, a_row_in_block, a_digit, wm, wn;
+};
+
+template <class RAW, class WT>
+__device__ __forceinline__ void dma_issue(const DmaCtx& c, int k0, RAW& raw, WT& wt) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) dma16(c.xsrc[j] + size_t(k0) * 8, &raw[(2 * (4 * c.wave + j)) * kRawRow]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) dma16(c.wsrc[j] + k0, &wt[(16 * (2 * c.wave + j)) * kBK]);
+}
+
+template <class RAW, class WT, class RAWN, class WTN>
+__device__ __forceinline__ void dma_step(const DmaCtx& c, bool next, int k_next, const RAW& raw, const WT& wt,
+                                         RAWN& raw_n, WTN& wt_n, uint8_t (&a_lds)[8][kBM][kPitch], int& colsum,
+                                         v16i (&acc)[4][2]) {
+  // this wave's DMAs for this step are done (none other is in flight yet);
+  // after the barrier every wave's are, and the previous step's reads are over
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (next) dma_issue(c, k_next, raw_n, wt_n);
+  // ---- raw shares -> 8 offset-binary digit planes
+  {
+    const uint4* rp = reinterpret_cast<const uint4*>(&raw[c.ar * kRawRow + c.ak * 8]);
+    const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
+    uint32_t d[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) d[e] ^= 0x80808080u;
+    uint32_t o[4][4];
+    transpose4(d[0], d[2], d[4], d[6], o[0][0], o[0][1], o[0][2], o[0][3]);
+    transpose4(d[8], d[10], d[12], d[14], o[1][0], o[1][1], o[1][2], o[1][3]);
+    transpose4(d[1], d[3], d[5], d[7], o[2][0], o[2][1], o[2][2], o[2][3]);
+    transpose4(d[9], d[11], d[13], d[15], o[3][0], o[3][1], o[3][2], o[3][3]);
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg) {
+      *reinterpret_cast<uint2*>(&a_lds[dg][c.ar][c.ak]) = make_uint2(o[0][dg], o[1][dg]);
+      *reinterpret_cast<uint2*>(&a_lds[dg + 4][c.ar][c.ak]) = make_uint2(o[2][dg], o[3][dg]);
+    }
+  }
+  // ---- column sums of the weight tile
+  {
+    const uint8_t* wrow = &wt[c.cl * kBK];
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const uint4 v = *reinterpret_cast<const uint4*>(wrow + (((2 * c.ch + cc) ^ (c.cl & 3)) * 16));
+      colsum = __builtin_amdgcn_sdot4(int(v.x), 0x01010101, colsum, false);
+      colsum = __builtin_amdgcn_sdot4(int(v.y), 0x01010101, colsum, false);
+      colsum = __builtin_amdgcn_sdot4(int(v.z), 0x01010101, colsum, false);
+      colsum = __builtin_amdgcn_sdot4(int(v.w), 0x01010101, colsum, false);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // ---- MFMA over the two 32-wide K steps
+#pragma unroll
+  for (int ks = 0; ks < kBK / 32; ++ks) {
+    const int chunk = ks * 2 + c.khalf;  // logical 16-byte chunk of the weight rows
+    v4i bop[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int row = c.wn * 64 + cb * 32 + c.i;
+      bop[cb] = *reinterpret_cast<const v4i*>(&wt[row * kBK + ((chunk ^ (row & 3)) * 16)]);
+    }
+    const int kb = ks * 32 + c.khalf * 16;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const v4i aop = *reinterpret_cast<const v4i*>(&a_lds[c.a_digit][c.wm * 16 + rb * 4 + c.a_row_in_block][kb]);
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        acc[rb][cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[cb], acc[rb][cb], 0, 0, 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    share_gemm_dma_kernel(const uint64_t* __restrict__ x, const int8_t* __restrict__ w,
+                          const int8_t* __restrict__ shifts, uint64_t* __restrict__ y, int M, int K, int N,
+                          uint64_t mask) {
+  __shared__ __attribute__((aligned(16))) uint8_t raw0[kBM * kRawRow];
+  __shared__ __attribute__((aligned(16))) uint8_t raw1[kBM * kRawRow];
+  __shared__ __attribute__((aligned(16))) uint8_t wt0[kBN * kBK];
+  __shared__ __attribute__((aligned(16))) uint8_t wt1[kBN * kBK];
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM][kPitch];
+  __shared__ int csum[kThreads];
+
+  const int t = threadIdx.x, lane = t & 63;
+  DmaCtx c;
+  c.wave = t >> 6;
+  c.wm = c.wave >> 1;
+  c.wn = c.wave & 1;
+  c.ar = t >> 3;  // transposer: raw row ar, shares ak..ak+7
+  c.ak = (t & 7) * 8;
+  c.cl = t >> 1;  // column sum: weight row cl, half ch
+  c.ch = t & 1;
+  c.i = lane & 31;
+  c.khalf = lane >> 5;
+  c.a_row_in_block = 2 * ((c.i >> 2) & 1) + (c.i >> 4);
+  c.a_digit = 4 * ((c.i >> 3) & 1) + (c.i & 3);
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  // DMA sources of this lane: 4 raw-share instructions (2 rows of 512 B each)
+  // and 2 weight instructions (16 rows of 64 B each) per wave and step.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 2 * (4 * c.wave + j) + (lane >> 5);
+    const int grow = min(m0 + row, M - 1);  // rows past M: any valid row, results dropped
+    c.xsrc[j] = reinterpret_cast<const uint8_t*>(x + size_t(grow) * K) + (lane & 31) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = 16 * (2 * c.wave + j) + (lane >> 2);
+    const int grow = min(n0 + row, N - 1);
+    const int ck = (lane & 3) ^ (row & 3);  // logical chunk stored at physical chunk lane & 3
+    c.wsrc[j] = w + size_t(grow) * K + ck * 16;
+  }
+  int colsum = 0;
+  v16i acc[4][2];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16i{0};
+
+  dma_issue(c, 0, raw0, wt0);
+  const int steps = K / kBK;
+  for (int s = 0; s < steps; s += 2) {
+    dma_step(c, s + 1 < steps, (s + 1) * kBK, raw0, wt0, raw1, wt1, a_lds, colsum, acc);
+    if (s + 1 < steps) dma_step(c, s + 2 < steps, (s + 2) * kBK, raw1, wt1, raw0, wt0, a_lds, colsum, acc);
+  }
+
+  // ---- epilogue: column sums, digit recombination, shift, mask
+  csum[t] = colsum;
+  __syncthreads();
+  const int i = c.i, khalf = c.khalf, wm = c.wm, wn = c.wn;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int c2 = wn * 64 + cb * 32 + i;
+    const int col = n0 + c2;
+    if (col >= N) continue;
+    const int64_t s_n = int64_t(csum[2 * c2]) + int64_t(csum[2 * c2 + 1]);
+    const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
+    const int sh = shifts ? int(shifts[col]) : 0;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int row = m0 + wm * 16 + rb * 4 + 2 * khalf + a;
+        if (row >= M) continue;
+        uint64_t v = corr;
+#pragma unroll
+        for (int dg = 0; dg < 8; ++dg) v += uint64_t(int64_t(acc[rb][cb][8 * a + dg])) << (8 * dg);
+        v = sh < 64 ? (v << sh) : 0;
+        y[size_t(row) * N + col] = v & mask;
+      }
+    }
+  }
+}
+
 hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
                              int M, int K, int N, int mask_bits, hipStream_t s) {
   const uint64_t mask = mask_bits >= 64 ? ~0ull : ((1ull << mask_bits) - 1);
@@ -231,6 +417,11 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
   // 16-byte weight loads need 16-byte aligned rows
   const int w_vec = (K % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
   if (w_bits == 8) {
+    if (K % kBK == 0 && w_vec && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+      hipLaunchKernelGGL(share_gemm_dma_kernel, grid, block, 0, s, x, static_cast<const int8_t*>(w), shifts, y, M,
+                         K, N, mask);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, 0, 0, w_vec);
     return hipGetLastError();
   }
