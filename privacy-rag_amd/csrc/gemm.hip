@@ -245,9 +245,7 @@ constexpr int kRawRow = kBK * 8;  // bytes of one raw share row per step
 // wave reads what was loaded.
 __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
   const unsigned lds = unsigned(reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)(lds_wave_base)));
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
-               "v"(src)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
 // One K step of the DMA path on stage buffers (raw, wt); the next step's DMAs
