@@ -138,6 +138,68 @@ void praghip_switch_destroy(praghip_switch_plan *plan);
 int praghip_share_gemm(int device, const uint64_t *x, const void *w, int w_bits, const int8_t *shifts,
                        uint64_t *y, size_t m, size_t k, size_t n, int mask_bits, void *stream);
 
+/* --------------------------------------------------------- ring ops (local) */
+/* LocalShares add / scale / layout / sum_rows (local_shares.hpp:22-32, kernels
+ * at local_shares.cu:9-12) on device buffers, asynchronous on `stream`, mod
+ * 2^mask_bits (59 = the reference ring).  add/scale: 16-byte aligned a, b, c
+ * [n].  layout: c[i] = a[map[i]] for i < n_out, map u64 device indices; an
+ * index >= n_in reads nothing and gives 0 (the reference rejects such a map on
+ * the host with E_CUDA_PUBLIC_MAP; the Python mirror does the same).
+ * sum_rows: out[r] = sum of the cols words of row r of a [rows][cols]. */
+int praghip_ring_add(int device, const uint64_t *a, const uint64_t *b, uint64_t *c, size_t n, int mask_bits,
+                     void *stream);
+int praghip_ring_scale(int device, const uint64_t *a, uint64_t factor, uint64_t *c, size_t n, int mask_bits,
+                       void *stream);
+int praghip_ring_layout(int device, const uint64_t *a, size_t n_in, const uint64_t *map, uint64_t *c, size_t n_out,
+                        void *stream);
+int praghip_ring_sum_rows(int device, const uint64_t *a, uint64_t *out, size_t rows, size_t cols, int mask_bits,
+                          void *stream);
+
+/* Centred lift of ring-2^59 words into RNS residues (matrix.cu:23-26 lift for
+ * width 0; resident.cu:23-30 lift for width > 0): out[b][k][z] = the signed
+ * value of v (v - 2^59 when bit 58 is set) mod q_k, canonical; for q_k > 2^59
+ * this is the reference's v + ((q_k - 2^59) & -(v >> 58)).  v = ring[b][z] (width 0, ring
+ * [blocks][2^log_n]) or v = ring[b][width-1-z] for z < width and 0 above
+ * (ring [blocks][width]).  out device [blocks][primes][2^log_n]. */
+int praghip_lift59(int device, const uint64_t *ring, uint64_t *out, size_t blocks, uint32_t log_n, size_t width,
+                   const uint64_t *q, size_t primes, void *stream);
+
+/* Dyadic multiply-accumulate, Barrett-128 (resident.cu:38-45 accumulate,
+ * matrix.cu:34-38 product): out[l][z] = sum_b a[b][l][z] * w[b][l % w_limbs][z]
+ * mod q[l % primes]; a [blocks][limbs][2^log_n], w [blocks][w_limbs][2^log_n],
+ * out [limbs][2^log_n], device. */
+int praghip_dyadic_mac(int device, const uint64_t *a, const uint64_t *w, uint64_t *out, size_t blocks, size_t limbs,
+                       uint32_t log_n, size_t w_limbs, const uint64_t *q, size_t primes, void *stream);
+
+/* Party-local dot product with BFV Delta scaling (resident.cu:60-74
+ * local_partials + local_scale, constants of resident/seal_adapter.cpp:43-53):
+ * m = (sum_j shares[s][j] * weights[j] mod 2^64) & (2^59 - 1), then
+ * scaled[s][k] = Delta_k * m + floor((r * m + 2^58) / 2^59) mod q_k, with
+ * delta[k] = floor(Q/2^59) mod q_k and r = Q mod 2^59.  shares
+ * [slots][words], weights [words], scaled [slots][primes], workspace of
+ * praghip_local_dot_workspace_words(slots) u64, all device. */
+size_t praghip_local_dot_workspace_words(size_t slots);
+int praghip_local_dot_scale(int device, const uint64_t *shares, const uint64_t *weights, size_t words, size_t slots,
+                            const uint64_t *delta, uint64_t r, const uint64_t *q, size_t primes, uint64_t *scaled,
+                            uint64_t *workspace, void *stream);
+
+/* ------------------------------------------------------------ weight files */
+/* The quantized_f12 int32 .npy weights (quantize_weights.py:60-64), read as
+ * MappedWeights does (artifacts.hpp:31-49): memory-mapped, version 1/2, '<i4',
+ * C order, exactly [rows][cols] ([rows] with vector != 0).  Errors: BAD_SHAPE,
+ * E_WEIGHT_FILE, E_WEIGHT_MAP, E_NPY_FORMAT, E_NPY_SHAPE.  at(): the ring word
+ * of artifacts.hpp:86-92 (sign-extended, & (2^59-1)).  upload(): copies the
+ * int32 [rows][cols] tensor to device memory (praghip_share_gemm, w_bits 32)
+ * and waits for the copy. */
+typedef struct praghip_weights praghip_weights;
+int praghip_weights_open(const char *path, size_t rows, size_t cols, int vector, praghip_weights **out);
+int praghip_weights_shape(const praghip_weights *w, size_t *rows, size_t *cols);
+const int32_t *praghip_weights_data(const praghip_weights *w);
+int praghip_weights_at(const praghip_weights *w, size_t row, size_t col, uint64_t *word);
+int praghip_weights_max_abs(const praghip_weights *w, uint64_t *max_abs);
+int praghip_weights_upload(const praghip_weights *w, int device, int32_t *dst, void *stream);
+void praghip_weights_close(praghip_weights *w);
+
 /* ------------------------------------------------------ synthetic inputs */
 /* Seeded counter-based inputs (no counterpart in the reference, whose probes
  * draw from mt19937_64, check_resident.cpp:26): element i of the buffer is

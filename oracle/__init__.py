@@ -60,6 +60,11 @@ def lib():
             "orc_lift59": (u64, [u64, u64]),
             "orc_dyadic_mac": (None, [vp, vp, vp, sz, sz, sz, sz, vp, sz]),
             "orc_local_dot_scale": (None, [vp, vp, sz, sz, vp, u64, vp, sz, vp]),
+            "orc_lift59_blocks": (None, [vp, vp, sz, sz, sz, vp, sz]),
+            "orc_ring_add": (None, [vp, vp, vp, sz, i32]),
+            "orc_ring_scale": (None, [vp, u64, vp, sz, i32]),
+            "orc_ring_layout": (None, [vp, sz, vp, vp, sz]),
+            "orc_ring_sum_rows": (None, [vp, vp, sz, sz, i32]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -230,4 +235,44 @@ def dyadic_mac(a: np.ndarray, w: np.ndarray, q) -> np.ndarray:
     wl = w.shape[1]
     out = np.empty((limbs, n), dtype=np.uint64)
     lib().orc_dyadic_mac(_p(a), _p(w), _p(out), blocks, limbs, n, len(q), _p(q), wl)
+    return out
+
+
+def lift59_blocks(ring: np.ndarray, q, n: int, width: int = 0) -> np.ndarray:
+    """[blocks][len(q)][n] lifted residues; ring is [blocks][n] (width 0) or [blocks][width]."""
+    ring = _u64(ring)
+    q = _u64(q)
+    per = width if width else n
+    blocks = ring.size // per
+    out = np.empty((blocks, len(q), n), dtype=np.uint64)
+    lib().orc_lift59_blocks(_p(ring), _p(out), blocks, n, width, _p(q), len(q))
+    return out
+
+
+def ring_add(a, b, bits: int = 59) -> np.ndarray:
+    a, b = _u64(a), _u64(b)
+    out = np.empty_like(a)
+    lib().orc_ring_add(_p(a), _p(b), _p(out), a.size, bits)
+    return out
+
+
+def ring_scale(a, k: int, bits: int = 59) -> np.ndarray:
+    a = _u64(a)
+    out = np.empty_like(a)
+    lib().orc_ring_scale(_p(a), int(k) & (2**64 - 1), _p(out), a.size, bits)
+    return out
+
+
+def ring_layout(a, index_map) -> np.ndarray:
+    a, m = _u64(a), _u64(index_map)
+    out = np.empty(m.size, dtype=np.uint64)
+    lib().orc_ring_layout(_p(a), a.size, _p(m), _p(out), m.size)
+    return out
+
+
+def ring_sum_rows(a, cols: int, bits: int = 59) -> np.ndarray:
+    a = _u64(a)
+    rows = a.size // cols
+    out = np.empty(rows, dtype=np.uint64)
+    lib().orc_ring_sum_rows(_p(a), _p(out), rows, cols, bits)
     return out

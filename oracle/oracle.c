@@ -467,10 +467,55 @@ int orc_share_gemm(const uint64_t *x, const void *w, int w_bits, const int8_t *s
 /* ------------------------------------------------------------------------ */
 /* Element-wise ops of the other backends.                                    */
 /* ------------------------------------------------------------------------ */
-/* Centred lift of a ring-2^59 word into Z_q (resident.cu:23-30, matrix.cu:23-26). */
+/* Centred lift of a ring-2^59 word into Z_q (resident.cu:23-30, matrix.cu:23-26):
+ * the signed value of v (v - 2^59 when bit 58 is set) as a canonical residue.
+ * For the reference's primes (q > 2^59) this is its branch-free
+ * v + ((q - 2^59) & -(v >> 58)); smaller primes take the remainder. */
 uint64_t orc_lift59(uint64_t v, uint64_t q) {
-  return v + ((q - (1ULL << 59)) & (0ULL - (v >> 58)));
+  if (q > (1ULL << 59)) return v + ((q - (1ULL << 59)) & (0ULL - (v >> 58)));
+  if (!(v >> 58)) return v % q;
+  const uint64_t d = ((1ULL << 59) - v) % q;
+  return d ? q - d : 0;
 }
+/* Centred lift over blocks (matrix.cu:23-26 for width 0, resident.cu:23-30
+ * for width > 0): out[b][k][z] = lift(v, q_k) with v = ring[b][z] (ring
+ * [blocks][n]) or v = ring[b][width-1-z] for z < width and 0 above (ring
+ * [blocks][width]). */
+void orc_lift59_blocks(const uint64_t *ring, uint64_t *out, size_t blocks, size_t n, size_t width,
+                       const uint64_t *q, size_t primes) {
+  for (size_t b = 0; b < blocks; ++b)
+    for (size_t k = 0; k < primes; ++k)
+      for (size_t z = 0; z < n; ++z) {
+        uint64_t v;
+        if (width == 0)
+          v = orc_lift59(ring[b * n + z], q[k]);
+        else
+          v = z < width ? orc_lift59(ring[b * width + (width - 1 - z)], q[k]) : 0;
+        out[(b * primes + k) * n + z] = v;
+      }
+}
+
+/* LocalShares ring ops (compute/local_shares.cu:9-12), mod 2^bits. */
+static uint64_t ring_mask_bits(int bits) { return bits >= 64 ? ~0ULL : (1ULL << bits) - 1; }
+void orc_ring_add(const uint64_t *a, const uint64_t *b, uint64_t *c, size_t n, int bits) {
+  for (size_t i = 0; i < n; ++i) c[i] = (a[i] + b[i]) & ring_mask_bits(bits);
+}
+void orc_ring_scale(const uint64_t *a, uint64_t k, uint64_t *c, size_t n, int bits) {
+  for (size_t i = 0; i < n; ++i) c[i] = (a[i] * k) & ring_mask_bits(bits);
+}
+/* layout: c[i] = a[map[i]]; an index out of range gives 0 here (the
+ * reference rejects such a map before any kernel runs). */
+void orc_ring_layout(const uint64_t *a, size_t n_in, const uint64_t *map, uint64_t *c, size_t n_out) {
+  for (size_t i = 0; i < n_out; ++i) c[i] = map[i] < n_in ? a[map[i]] : 0;
+}
+void orc_ring_sum_rows(const uint64_t *a, uint64_t *out, size_t rows, size_t cols, int bits) {
+  for (size_t r = 0; r < rows; ++r) {
+    uint64_t x = 0;
+    for (size_t i = 0; i < cols; ++i) x += a[r * cols + i];
+    out[r] = x & ring_mask_bits(bits);
+  }
+}
+
 /* Dyadic multiply-accumulate out = sum_b a_b (.) w_b mod q with Barrett-128
  * (resident.cu:38-45 accumulate, matrix.cu:34-38 product). a is
  * [blocks][limbs][N], w is [blocks][primes][N] broadcast over the limbs whose

@@ -32,6 +32,14 @@ int fail(int code, const std::string& text) {
   g_error = text;
   return code;
 }
+}  // namespace
+
+// The error slot, for the other host-side sources of the library.
+namespace praghip {
+int set_error(int code, const std::string& text) { return fail(code, text); }
+}  // namespace praghip
+
+namespace {
 
 // ------------------------------------------------------------ number theory
 uint64_t mulmod(uint64_t a, uint64_t b, uint64_t q) { return uint64_t((u128)a * b % q); }
@@ -805,6 +813,136 @@ int praghip_fill_i8(int device, int8_t* data, size_t count, uint64_t seed, void*
   if (e == hipSuccess) e = launch_fill_i8(data, count, seed, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_FILL_HIP: ") + hipGetErrorString(e));
   return PRAGHIP_OK;
+}
+
+}  // extern "C"
+
+// ======================================================== share-side kernels
+namespace {
+// q must be an odd prime-sized modulus below 2^62 (Barrett-128 and the lift's
+// q - 2^59 need q > 2^59 only for the reference's own primes; any q works).
+bool valid_moduli(const uint64_t* q, size_t primes) {
+  if (!q || primes < 1 || primes > size_t(kMaxKeyPrimes)) return false;
+  for (size_t i = 0; i < primes; ++i)
+    if (q[i] < 3 || q[i] >= (1ull << 62) || !(q[i] & 1)) return false;
+  return true;
+}
+Barrett barrett_of(uint64_t q) {
+  const u128 ratio = (~(u128)0) / q;
+  return Barrett{q, uint64_t(ratio), uint64_t(ratio >> 64)};
+}
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
+int hip_fail(const char* what, hipError_t e) { return fail(PRAGHIP_E_DEVICE, std::string(what) + hipGetErrorString(e)); }
+}  // namespace
+
+extern "C" {
+
+int praghip_ring_add(int device, const uint64_t* a, const uint64_t* b, uint64_t* c, size_t n, int mask_bits,
+                     void* stream) {
+  if (n == 0) return PRAGHIP_OK;
+  if (!a || !b || !c) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
+  if (!aligned8(a) || !aligned8(b) || !aligned8(c) ||
+      ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15))
+    return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_ring_add(a, b, c, n, mask_bits, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_CUDA_LOCAL: ", e);
+}
+
+int praghip_ring_scale(int device, const uint64_t* a, uint64_t factor, uint64_t* c, size_t n, int mask_bits,
+                       void* stream) {
+  if (n == 0) return PRAGHIP_OK;
+  if (!a || !c) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(c)) & 15)
+    return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_ring_scale(a, factor, c, n, mask_bits, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_CUDA_LOCAL: ", e);
+}
+
+int praghip_ring_layout(int device, const uint64_t* a, size_t n_in, const uint64_t* map, uint64_t* c, size_t n_out,
+                        void* stream) {
+  if (n_out == 0) return PRAGHIP_OK;
+  if (!a || !map || !c) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (n_in == 0) return fail(PRAGHIP_E_SHAPE, "E_CUDA_SHAPE");
+  if (!aligned8(a) || !aligned8(map) || !aligned8(c)) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_ring_layout(a, n_in, map, c, n_out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_CUDA_LOCAL: ", e);
+}
+
+int praghip_ring_sum_rows(int device, const uint64_t* a, uint64_t* out, size_t rows, size_t cols, int mask_bits,
+                          void* stream) {
+  if (rows == 0) return PRAGHIP_OK;
+  if (!a || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (cols == 0) return fail(PRAGHIP_E_SHAPE, "E_CUDA_SHAPE");
+  if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
+  if (!aligned8(a) || !aligned8(out)) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_ring_sum_rows(a, out, rows, cols, mask_bits, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_CUDA_LOCAL: ", e);
+}
+
+int praghip_lift59(int device, const uint64_t* ring, uint64_t* out, size_t blocks, uint32_t log_n, size_t width,
+                   const uint64_t* q, size_t primes, void* stream) {
+  if (blocks == 0) return PRAGHIP_OK;
+  if (!ring || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (!valid_moduli(q, primes) || log_n < 1 || log_n > 17 || width > (size_t(1) << log_n))
+    return fail(PRAGHIP_E_SHAPE, "E_LIFT_SHAPE");
+  if (!aligned8(ring) || !aligned8(out)) return fail(PRAGHIP_E_ARGUMENT, "E_LIFT_ALIGNMENT");
+  PrimeList pl{};
+  for (size_t i = 0; i < primes; ++i) pl.q[i] = q[i];
+  pl.count = int(primes);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_lift59(ring, out, blocks, int(log_n), width, pl, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_LIFT_HIP: ", e);
+}
+
+int praghip_dyadic_mac(int device, const uint64_t* a, const uint64_t* w, uint64_t* out, size_t blocks, size_t limbs,
+                       uint32_t log_n, size_t w_limbs, const uint64_t* q, size_t primes, void* stream) {
+  if (limbs == 0) return PRAGHIP_OK;
+  if (!a || !w || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (!valid_moduli(q, primes) || blocks == 0 || w_limbs == 0 || log_n < 1 || log_n > 17)
+    return fail(PRAGHIP_E_SHAPE, "E_DYADIC_SHAPE");
+  if (!aligned8(a) || !aligned8(w) || !aligned8(out)) return fail(PRAGHIP_E_ARGUMENT, "E_DYADIC_ALIGNMENT");
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < primes; ++i) m[i] = barrett_of(q[i]);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess)
+    e = launch_dyadic_mac(a, w, out, blocks, limbs, int(log_n), w_limbs, m, int(primes),
+                          static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_DYADIC_HIP: ", e);
+}
+
+size_t praghip_local_dot_workspace_words(size_t slots) { return slots * kLocalTiles; }
+
+int praghip_local_dot_scale(int device, const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,
+                            const uint64_t* delta, uint64_t r, const uint64_t* q, size_t primes, uint64_t* scaled,
+                            uint64_t* workspace, void* stream) {
+  if (slots == 0) return PRAGHIP_OK;
+  if (!shares || !weights || !delta || !scaled || !workspace) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (!valid_moduli(q, primes) || words == 0 || slots > 65535 || r >= (1ull << 59))
+    return fail(PRAGHIP_E_SHAPE, "E_LOCAL_SHAPE");
+  for (size_t k = 0; k < primes; ++k)
+    if (delta[k] >= q[k]) return fail(PRAGHIP_E_CANONICAL, "E_LOCAL_DELTA");
+  if (!aligned8(shares) || !aligned8(weights) || !aligned8(scaled) || !aligned8(workspace))
+    return fail(PRAGHIP_E_ARGUMENT, "E_LOCAL_ALIGNMENT");
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < primes; ++i) m[i] = barrett_of(q[i]);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess)
+    e = launch_local_dot_scale(shares, weights, words, slots, delta, r, m, int(primes), scaled, workspace,
+                               static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_LOCAL_HIP: ", e);
 }
 
 }  // extern "C"

@@ -67,6 +67,22 @@ hipError_t launch_fill_residues(uint64_t* out, size_t words, int log_n, const Pr
 hipError_t launch_fill_u64(uint64_t* out, size_t count, uint64_t seed, hipStream_t s);
 hipError_t launch_fill_i8(int8_t* out, size_t count, uint64_t seed, hipStream_t s);
 
+// Ring ops, lift, dyadic MAC and local dot (shares.hip).
+constexpr unsigned kLocalTiles = 256;  // workgroups per slot of the local dot (workspace words per slot)
+hipError_t launch_ring_add(const uint64_t* a, const uint64_t* b, uint64_t* c, size_t n, int bits, hipStream_t s);
+hipError_t launch_ring_scale(const uint64_t* a, uint64_t factor, uint64_t* c, size_t n, int bits, hipStream_t s);
+hipError_t launch_ring_layout(const uint64_t* a, size_t n_in, const uint64_t* map, uint64_t* c, size_t n_out,
+                              hipStream_t s);
+hipError_t launch_ring_sum_rows(const uint64_t* a, uint64_t* out, size_t rows, size_t cols, int bits,
+                                hipStream_t s);
+hipError_t launch_lift59(const uint64_t* ring, uint64_t* out, size_t blocks, int log_n, size_t width,
+                         const PrimeList& q, hipStream_t s);
+hipError_t launch_dyadic_mac(const uint64_t* a, const uint64_t* w, uint64_t* out, size_t blocks, size_t limbs,
+                             int log_n, size_t w_limbs, const Barrett* m, int primes, hipStream_t s);
+hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,
+                                  const uint64_t* delta, uint64_t r, const Barrett* m, int primes, uint64_t* scaled,
+                                  uint64_t* work, hipStream_t s);
+
 hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
                             hipStream_t s);
 // Workgroups of the fused keyswitch kernel for 2^log_n (the acc slots a plan

@@ -367,7 +367,7 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
   using S = Passes<LOGN>;
   constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
   if constexpr (P + 1 < S::NP) {
-    constexpr int LO1 = S::lo(INV, P + 1), R1 = S::r(INV, P + 1);
+    constexpr int R1 = S::r(INV, P + 1);
     typename A::TW wn[pass_twiddles<R1>()];
     auto prefetch = [&] {
       if constexpr (A::kAhead) load_pass_twiddles<LOGN, INV, P + 1>(wn, t, tab);

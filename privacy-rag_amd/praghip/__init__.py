@@ -8,6 +8,9 @@ libpraghip.so:
 * :class:`Switch`    - prag::experimental_full_switch::Switch (switch.hpp:12-28)
 * :func:`share_gemm` - the party-local share GEMM (bfv_matrix.inc:101-105),
   offered as a LocalShares operation (local_shares.hpp:22-32)
+* :class:`LocalShares` and the ring ops, :func:`lift59`, :func:`dyadic_mac`,
+  :func:`local_dot_scale` - compute/local_shares.cu, resident.cu, matrix.cu
+* :class:`MappedWeights` - the int32 .npy weight reader (artifacts.hpp:31-49)
 
 Device data is handed over as torch tensors on the GPU (int64 or uint64 with
 u64 bit patterns); torch is used only for memory and streams.
@@ -15,7 +18,9 @@ u64 bit patterns); torch is used only for memory and streams.
 from ._lib import Cleanup, PraghipError, Timing, check, lib  # noqa: F401
 from .ntt import NttBatch, ntt_tables  # noqa: F401
 from .keyswitch import Switch  # noqa: F401
-from .shares import share_gemm  # noqa: F401
+from .shares import (LocalShares, bfv_delta, dyadic_mac, lift59, local_dot_scale, ring_add,  # noqa: F401
+                     ring_layout, ring_scale, ring_sum_rows, share_gemm)
+from .weights import MappedWeights  # noqa: F401
 from . import synth  # noqa: F401
 
 

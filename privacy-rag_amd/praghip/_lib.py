@@ -58,6 +58,21 @@ SIGNATURES = {
     "praghip_switch_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_switch_destroy": (None, [vp]),
     "praghip_share_gemm": (i32, [i32, vp, vp, i32, vp, vp, sz, sz, sz, i32, vp]),
+    "praghip_ring_add": (i32, [i32, vp, vp, vp, sz, i32, vp]),
+    "praghip_ring_scale": (i32, [i32, vp, u64, vp, sz, i32, vp]),
+    "praghip_ring_layout": (i32, [i32, vp, sz, vp, vp, sz, vp]),
+    "praghip_ring_sum_rows": (i32, [i32, vp, vp, sz, sz, i32, vp]),
+    "praghip_lift59": (i32, [i32, vp, vp, sz, u32, sz, vp, sz, vp]),
+    "praghip_dyadic_mac": (i32, [i32, vp, vp, vp, sz, sz, u32, sz, vp, sz, vp]),
+    "praghip_local_dot_workspace_words": (sz, [sz]),
+    "praghip_local_dot_scale": (i32, [i32, vp, vp, sz, sz, vp, u64, vp, sz, vp, vp, vp]),
+    "praghip_weights_open": (i32, [ctypes.c_char_p, sz, sz, i32, pp]),
+    "praghip_weights_shape": (i32, [vp, ctypes.POINTER(sz), ctypes.POINTER(sz)]),
+    "praghip_weights_data": (vp, [vp]),
+    "praghip_weights_at": (i32, [vp, sz, sz, ctypes.POINTER(u64)]),
+    "praghip_weights_max_abs": (i32, [vp, ctypes.POINTER(u64)]),
+    "praghip_weights_upload": (i32, [vp, i32, vp, vp]),
+    "praghip_weights_close": (None, [vp]),
     "praghip_fill_residues": (i32, [i32, vp, sz, u32, vp, sz, u64, vp]),
     "praghip_fill_u64": (i32, [i32, vp, sz, u64, vp]),
     "praghip_fill_i8": (i32, [i32, vp, sz, u64, vp]),

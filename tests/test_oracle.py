@@ -279,3 +279,45 @@ def test_dyadic_mac_closed_form():
         ql = q[l % 3]
         want = [sum(int(a[b, l, z]) * int(w[b, l % 3, z]) for b in range(blocks)) % ql for z in range(n)]
         assert got[l].tolist() == want, l
+
+
+def test_ring_ops_closed_form():
+    """LocalShares ring ops against Python integers mod 2^59 (and 2^64), including
+    words at the mask edge, so a missing mask or a wrong width shows."""
+    t59 = (1 << 59) - 1
+    a = oracle.fill_u64(37, 31) & np.uint64(t59)
+    b = oracle.fill_u64(37, 32) & np.uint64(t59)
+    a[:3] = [t59, t59, 0]
+    b[:3] = [t59, 1, 0]
+    for bits in (59, 64):
+        m = (1 << bits) - 1
+        assert oracle.ring_add(a, b, bits).tolist() == [(int(x) + int(y)) & m for x, y in zip(a, b)]
+        k = (1 << 58) + 3
+        assert oracle.ring_scale(a, k, bits).tolist() == [(int(x) * k) & m for x in a]
+        rows = oracle.ring_sum_rows(a[:36], 9, bits)
+        assert rows.tolist() == [sum(int(x) for x in a[9 * r:9 * r + 9]) & m for r in range(4)]
+    idx = np.array([5, 0, 36, 36, 2, 40], dtype=np.uint64)
+    assert oracle.ring_layout(a, idx).tolist() == [int(a[5]), int(a[0]), int(a[36]), int(a[36]), int(a[2]), 0]
+
+
+def test_lift_blocks_layouts():
+    """Block lift: width 0 is the element-wise lift per prime (matrix.cu); width > 0
+    reverses each block of `width` words and pads with zeros (resident.cu)."""
+    q = [cf.LOCKED_PRIMES[0], cf.primes_below(50, 64, 1)[0]]
+    t = 1 << 59
+    ring = oracle.fill_u64(3 * 16, 41) & np.uint64(t - 1)
+    ring[:4] = [(1 << 58) - 1, 1 << 58, t - 1, 0]
+    out = oracle.lift59_blocks(ring, q, 16)
+    for b in range(3):
+        for k, qk in enumerate(q):
+            for z in range(16):
+                v = int(ring[b * 16 + z])
+                assert int(out[b, k, z]) == (v - t if v >> 58 else v) % qk
+    ring5 = ring[:10]
+    out = oracle.lift59_blocks(ring5, q, 16, width=5)
+    for b in range(2):
+        for k, qk in enumerate(q):
+            for z in range(16):
+                v = int(ring5[b * 5 + 4 - z]) if z < 5 else None
+                want = 0 if v is None else (v - t if v >> 58 else v) % qk
+                assert int(out[b, k, z]) == want
