@@ -158,6 +158,22 @@ def bench_gemm(torch, praghip, steps, warmup):
     }
 
 
+def bench_qwen3(torch, praghip, steps, warmup):
+    """Every local share GEMM of a Qwen3-0.6B forward over 512 tokens: 28 layers x
+    {joint q|k|v 1024->4096, o 2048->1024, joint gate|up 1024->6144, down 3072->1024},
+    int8 weights with per-channel shifts, one batched call per forward."""
+    m = praghip.Qwen3LocalGemms(rows=512)
+    ms = Timer(torch).run(m.forward, steps, warmup)
+    tops = m.ops / (ms * 1e-3) / 1e12
+    return {"layers": m.shape.layers, "rows": m.rows, "ms_per_forward": ms, "ms_per_step": ms,
+            "layers_per_s": m.shape.layers / (ms * 1e-3), "tops": tops,
+            "ops_per_forward": m.ops,
+            "roofline": {"bound": "mfma", "achieved": round(8 * tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
+                         "frac": round(8 * tops / I8_PEAK_TOPS, 4), "traffic": None,
+                         "kernel": "share_gemm_dma_kernel over the 112 products (i8 MFMA ops executed)"},
+            "_model": m}
+
+
 def bench_copy(torch, steps, warmup):
     """Plain device copy of 384 MiB (the bytes one NTT launch reads, and again writes):
     the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -227,7 +243,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "qwen3", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
     args = ap.parse_args()
@@ -259,6 +275,12 @@ def main() -> int:
         log("share GEMM 512x1024x3072 ...")
         res["gemm"] = bench_gemm(torch, praghip, args.steps, args.warmup)
         log(f"GEMM {res['gemm']['tops']:.4g} TOPS")
+    if args.only in ("all", "qwen3"):
+        log("Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens ...")
+        res["qwen3"] = bench_qwen3(torch, praghip, args.steps, args.warmup)
+        log(f"Qwen3 forward {res['qwen3']['ms_per_forward']:.3f} ms, {res['qwen3']['tops']:.4g} TOPS")
+        if args.only == "all":
+            del res["qwen3"]["_model"]  # free its 2.7 GB before the CPU leg
     cpu = {}
     if not args.no_cpu and args.only == "all":
         log("oracle CPU baselines ...")
@@ -268,11 +290,11 @@ def main() -> int:
     def clean(d):
         return {k: v for k, v in d.items() if not k.startswith("_")}
 
-    primary = res.get("ntt") or res.get("keyswitch") or res.get("gemm")
-    key = "ntt" if "ntt" in res else ("keyswitch" if "keyswitch" in res else "gemm")
+    key = next(k for k in ("ntt", "keyswitch", "gemm", "qwen3") if k in res)
+    primary = res[key]
     value = {"ntt": lambda r: r["ntt_per_s"], "keyswitch": lambda r: r["keyswitch_per_s"],
-             "gemm": lambda r: r["tops"]}[key](primary)
-    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "gemm": "TOPS"}[key]
+             "gemm": lambda r: r["tops"], "qwen3": lambda r: r["tops"]}[key](primary)
+    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "gemm": "TOPS", "qwen3": "TOPS"}[key]
     line = {
         "metric": METRIC,
         "value": value,
@@ -284,13 +306,14 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64" if key == "ntt" else ("u64+f64" if key == "keyswitch" else "i8"),
+        "dtype": {"ntt": "f64", "keyswitch": "u64+f64"}.get(key, "i8"),
         "data": "synthetic (seeded splitmix64 on the GPU)",
         "config": {"workload": {
             "ntt": "batched forward+inverse negacyclic NTT, N=16384, 6 primes ~50 bit, "
                    "256 ciphertexts x 2 polynomials = 3072 limbs",
             "keyswitch": "keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
-            "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64"}[key],
+            "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64",
+            "qwen3": "Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens"}[key],
             "N": N, "parallelism": "single GPU"},
         "roofline": primary["roofline"],
         "cpu_baseline": cpu.get(key),

@@ -138,6 +138,21 @@ void praghip_switch_destroy(praghip_switch_plan *plan);
 int praghip_share_gemm(int device, const uint64_t *x, const void *w, int w_bits, const int8_t *shifts,
                        uint64_t *y, size_t m, size_t k, size_t n, int mask_bits, void *stream);
 
+/* A list of share GEMMs launched in order on one stream, for the per-layer
+ * projections of Transformer::project_many / project_joint_many
+ * (model.hpp:66-126): the joint q/k/v and gate/up products, o and down.  Each
+ * entry has the meaning of praghip_share_gemm's arguments; the whole list is
+ * validated before the first launch. */
+typedef struct praghip_gemm_desc {
+  const uint64_t *x;
+  const void *w;
+  const int8_t *shifts;
+  uint64_t *y;
+  size_t m, k, n;
+  int w_bits, mask_bits;
+} praghip_gemm_desc;
+int praghip_share_gemm_batch(int device, const praghip_gemm_desc *list, size_t count, void *stream);
+
 /* --------------------------------------------------------- ring ops (local) */
 /* LocalShares add / scale / layout / sum_rows (local_shares.hpp:22-32, kernels
  * at local_shares.cu:9-12) on device buffers, asynchronous on `stream`, mod
@@ -204,11 +219,12 @@ void praghip_weights_close(praghip_weights *w);
 /* Seeded counter-based inputs (no counterpart in the reference, whose probes
  * draw from mt19937_64, check_resident.cpp:26): element i of the buffer is
  * splitmix64(seed + (i+1)*0x9E3779B97F4A7C15).  Residues: mulhi(z, q[limb % primes])
- * over device [limbs][2^log_n]; u64: z; int8: mulhi(z, 255) - 127. */
+ * over device [limbs][2^log_n]; u64: z; int8: mulhi(z, 255) - 127; shifts: mulhi(z, 8). */
 int praghip_fill_residues(int device, uint64_t *data, size_t limbs, uint32_t log_n, const uint64_t *q,
                           size_t primes, uint64_t seed, void *stream);
 int praghip_fill_u64(int device, uint64_t *data, size_t count, uint64_t seed, void *stream);
 int praghip_fill_i8(int device, int8_t *data, size_t count, uint64_t seed, void *stream);
+int praghip_fill_shift(int device, int8_t *data, size_t count, uint64_t seed, void *stream);  /* mulhi(z, 8) */
 
 #ifdef __cplusplus
 }

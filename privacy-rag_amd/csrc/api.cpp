@@ -777,6 +777,32 @@ int praghip_share_gemm(int device, const uint64_t* x, const void* w, int w_bits,
   return PRAGHIP_OK;
 }
 
+int praghip_share_gemm_batch(int device, const praghip_gemm_desc* list, size_t count, void* stream) {
+  if (count == 0) return PRAGHIP_OK;
+  if (!list) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  for (size_t i = 0; i < count; ++i) {  // validate the whole list before the first launch
+    const praghip_gemm_desc& d = list[i];
+    if (d.m == 0 || d.n == 0) continue;
+    if (!d.x || !d.w || !d.y) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+    if (d.w_bits != 8 && d.w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
+    if (d.mask_bits < 1 || d.mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
+    if (d.k >= (1u << 17) || d.m >= (1u << 31) || d.n >= (1u << 31)) return fail(PRAGHIP_E_SHAPE, "E_SHARE_SHAPE");
+    if ((reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.y)) & 7 ||
+        (d.w_bits == 32 && (reinterpret_cast<uintptr_t>(d.w) & 3)))
+      return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  }
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  for (size_t i = 0; i < count && e == hipSuccess; ++i) {
+    const praghip_gemm_desc& d = list[i];
+    if (d.m == 0 || d.n == 0) continue;
+    e = launch_share_gemm(d.x, d.w, d.w_bits, d.shifts, d.y, int(d.m), int(d.k), int(d.n), d.mask_bits,
+                          static_cast<hipStream_t>(stream));
+  }
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_SHARE_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
 }  // extern "C"
 
 // ========================================================= synthetic inputs
@@ -802,6 +828,15 @@ int praghip_fill_u64(int device, uint64_t* data, size_t count, uint64_t seed, vo
   DeviceScope scope(device);
   hipError_t e = scope.status();
   if (e == hipSuccess) e = launch_fill_u64(data, count, seed, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_FILL_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
+int praghip_fill_shift(int device, int8_t* data, size_t count, uint64_t seed, void* stream) {
+  if (!data && count) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_fill_shift(data, count, seed, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_FILL_HIP: ") + hipGetErrorString(e));
   return PRAGHIP_OK;
 }

@@ -27,6 +27,12 @@ __global__ void fill_i8_kernel(int8_t* __restrict__ out, size_t count, uint64_t 
     out[i] = int8_t(int64_t(__umul64hi(splitmix64(seed, i), 255)) - 127);
 }
 
+// Per-channel shifts in [0, 7]: mulhi(z, 8).
+__global__ void fill_shift_kernel(int8_t* __restrict__ out, size_t count, uint64_t seed) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x)
+    out[i] = int8_t(__umul64hi(splitmix64(seed, i), 8));
+}
+
 static unsigned grid_of(size_t n) { return unsigned(std::min<size_t>((n + 255) / 256, 1u << 16)); }
 
 hipError_t launch_fill_residues(uint64_t* out, size_t words, int log_n, const PrimeList& q, uint64_t seed,
@@ -43,6 +49,12 @@ hipError_t launch_fill_u64(uint64_t* out, size_t count, uint64_t seed, hipStream
 hipError_t launch_fill_i8(int8_t* out, size_t count, uint64_t seed, hipStream_t s) {
   if (!count) return hipSuccess;
   hipLaunchKernelGGL(fill_i8_kernel, dim3(grid_of(count)), dim3(256), 0, s, out, count, seed);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_shift(int8_t* out, size_t count, uint64_t seed, hipStream_t s) {
+  if (!count) return hipSuccess;
+  hipLaunchKernelGGL(fill_shift_kernel, dim3(grid_of(count)), dim3(256), 0, s, out, count, seed);
   return hipGetLastError();
 }
 

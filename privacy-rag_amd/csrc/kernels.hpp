@@ -66,6 +66,7 @@ hipError_t launch_fill_residues(uint64_t* out, size_t words, int log_n, const Pr
                                 hipStream_t s);
 hipError_t launch_fill_u64(uint64_t* out, size_t count, uint64_t seed, hipStream_t s);
 hipError_t launch_fill_i8(int8_t* out, size_t count, uint64_t seed, hipStream_t s);
+hipError_t launch_fill_shift(int8_t* out, size_t count, uint64_t seed, hipStream_t s);
 
 // Ring ops, lift, dyadic MAC and local dot (shares.hip).
 constexpr unsigned kLocalTiles = 256;  // workgroups per slot of the local dot (workspace words per slot)

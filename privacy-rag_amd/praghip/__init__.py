@@ -11,6 +11,8 @@ libpraghip.so:
 * :class:`LocalShares` and the ring ops, :func:`lift59`, :func:`dyadic_mac`,
   :func:`local_dot_scale` - compute/local_shares.cu, resident.cu, matrix.cu
 * :class:`MappedWeights` - the int32 .npy weight reader (artifacts.hpp:31-49)
+* :class:`Qwen3LocalGemms` - the local products of a Qwen3 forward
+  (model.hpp:66-126) as one batched call
 
 Device data is handed over as torch tensors on the GPU (int64 or uint64 with
 u64 bit patterns); torch is used only for memory and streams.
@@ -21,6 +23,7 @@ from .keyswitch import Switch  # noqa: F401
 from .shares import (LocalShares, bfv_delta, dyadic_mac, lift59, local_dot_scale, ring_add,  # noqa: F401
                      ring_layout, ring_scale, ring_sum_rows, share_gemm)
 from .weights import MappedWeights  # noqa: F401
+from .qwen3 import QWEN3_0_6B, Qwen3LocalGemms, Qwen3Shape  # noqa: F401
 from . import synth  # noqa: F401
 
 

@@ -33,6 +33,13 @@ class Timing(ctypes.Structure):
 
 
 vp, sz, u32, u64, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+
+
+class GemmDesc(ctypes.Structure):
+    """praghip_gemm_desc (include/praghip.h)."""
+    _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("shifts", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("m", ctypes.c_size_t), ("k", ctypes.c_size_t), ("n", ctypes.c_size_t),
+                ("w_bits", ctypes.c_int), ("mask_bits", ctypes.c_int)]
 pp = ctypes.POINTER(ctypes.c_void_p)
 
 SIGNATURES = {
@@ -76,6 +83,8 @@ SIGNATURES = {
     "praghip_fill_residues": (i32, [i32, vp, sz, u32, vp, sz, u64, vp]),
     "praghip_fill_u64": (i32, [i32, vp, sz, u64, vp]),
     "praghip_fill_i8": (i32, [i32, vp, sz, u64, vp]),
+    "praghip_fill_shift": (i32, [i32, vp, sz, u64, vp]),
+    "praghip_share_gemm_batch": (i32, [i32, vp, sz, vp]),
 }
 
 _lib = None

@@ -28,3 +28,11 @@ def fill_i8(t, seed: int, stream=None):
     check(lib().praghip_fill_i8(t.device.index or 0, dev_ptr(t, (torch.int8,)), t.numel(), seed,
                                 stream_handle(stream)))
     return t
+
+
+def fill_shift(t, seed: int, stream=None):
+    """Per-channel shifts in [0, 7] (int8)."""
+    import torch
+    check(lib().praghip_fill_shift(t.device.index or 0, dev_ptr(t, (torch.int8,)), t.numel(), seed,
+                                   stream_handle(stream)))
+    return t
