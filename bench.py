@@ -153,7 +153,7 @@ def bench_gemm(torch, praghip, steps, warmup):
         "shape": [m, k, n], "ms_per_step": ms, "tops": tops,
         "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm", 1),
-                     "kernel": "share_gemm_kernel<8> (i8 MFMA ops executed)"},
+                     "kernel": "share_gemm_dma_kernel (i8 MFMA ops executed)"},
         "_tensors": (x, w, y),
     }
 
@@ -169,8 +169,9 @@ def bench_qwen3(torch, praghip, steps, warmup):
             "layers_per_s": m.shape.layers / (ms * 1e-3), "tops": tops,
             "ops_per_forward": m.ops,
             "roofline": {"bound": "mfma", "achieved": round(8 * tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
-                         "frac": round(8 * tops / I8_PEAK_TOPS, 4), "traffic": None,
-                         "kernel": "share_gemm_dma_kernel over the 112 products (i8 MFMA ops executed)"},
+                         "frac": round(8 * tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("qwen3", 1),
+                         "kernel": "share_gemm_dma_kernel over the 112 products (i8 MFMA ops executed); "
+                                   "traffic is the average per product"},
             "_model": m}
 
 
