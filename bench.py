@@ -235,7 +235,21 @@ def cpu_baselines(torch, res, budget_s: float):
     out["gemm_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
     out["gemm"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
                    "sample": f"{rows} of 512 activation rows x 1024 x 3072"}
-    # NTT parity on a slice of the timed batch
+    # Qwen3: the four products of layer 0 on 16 of the 512 token rows
+    if "qwen3" in res and "_sample" in res["qwen3"]:
+        ok, ops, dt = True, 0, 0.0
+        for x_t, w_t, sh_t, y_t in res["qwen3"]["_sample"]:
+            x = x_t.numpy().view(np.uint64)
+            w = w_t.numpy()
+            sh = None if sh_t is None else sh_t.numpy()
+            t0 = time.perf_counter()
+            y = oracle.share_gemm(x, w, sh, mask_bits=64, threads=threads)
+            dt += time.perf_counter() - t0
+            ops += 2 * x.shape[0] * x.shape[1] * w.shape[0]
+            ok &= bool(np.array_equal(y, y_t.numpy().view(np.uint64)))
+        out["qwen3_parity"] = ok
+        out["qwen3"] = {"value": ops / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+                        "sample": "layer 0, 16 of 512 token rows, all four products (q|k|v, o, gate|up, down)"}
     return out
 
 
@@ -281,7 +295,14 @@ def main() -> int:
         res["qwen3"] = bench_qwen3(torch, praghip, args.steps, args.warmup)
         log(f"Qwen3 forward {res['qwen3']['ms_per_forward']:.3f} ms, {res['qwen3']['tops']:.4g} TOPS")
         if args.only == "all":
-            del res["qwen3"]["_model"]  # free its 2.7 GB before the CPU leg
+            # keep 16 rows of layer 0 on the host for the CPU leg, free the 2.7 GB model
+            m = res["qwen3"].pop("_model")
+            sample = []
+            for name, _, _ in m.shape.products():
+                x, w, sh, y = m.product(0, name)
+                sample.append((x[:16].cpu(), w.cpu(), None if sh is None else sh.cpu(), y[:16].cpu()))
+            res["qwen3"]["_sample"] = sample
+            del m
     cpu = {}
     if not args.no_cpu and args.only == "all":
         log("oracle CPU baselines ...")

@@ -88,3 +88,42 @@ def test_no_device_here_is_reported():
     with pytest.raises(praghip.PraghipError) as e:
         praghip.NttBatch([cf.LOCKED_PRIMES[0]], 14)
     assert e.value.code == _lib.E_DEVICE and "E_GFX950_REQUIRED" in e.value.text
+
+
+def test_share_entry_points_validate_before_device():
+    """The ring ops, lift, dyadic MAC, local dot and batched GEMM reject bad
+    arguments before any device call (fake, aligned addresses are never touched)."""
+    import ctypes
+
+    import numpy as np
+    L = _lib.lib()
+    A = 1 << 20  # 16-byte aligned fake device address
+    q = np.array(cf.LOCKED_PRIMES[:2], dtype=np.uint64)
+
+    def code(rc):
+        return rc, L.praghip_last_error().decode()
+
+    assert code(L.praghip_ring_add(0, A, A, A, 8, 0, None)) == (_lib.E_ARGUMENT, "E_SHARE_MASK")
+    assert code(L.praghip_ring_add(0, A + 8, A, A, 8, 59, None)) == (_lib.E_ARGUMENT, "E_SHARE_ALIGNMENT")
+    assert code(L.praghip_ring_add(0, None, A, A, 8, 59, None)) == (_lib.E_ARGUMENT, "E_NULL")
+    assert L.praghip_ring_add(0, None, None, None, 0, 59, None) == _lib.OK  # empty is a no-op
+    assert code(L.praghip_ring_scale(0, A, 3, A, 8, 65, None)) == (_lib.E_ARGUMENT, "E_SHARE_MASK")
+    assert code(L.praghip_ring_layout(0, A, 0, A, A, 4, None)) == (_lib.E_SHAPE, "E_CUDA_SHAPE")
+    assert code(L.praghip_ring_sum_rows(0, A, A, 4, 0, 59, None)) == (_lib.E_SHAPE, "E_CUDA_SHAPE")
+    assert code(L.praghip_lift59(0, A, A, 1, 12, 5000, q.ctypes.data, 2, None)) == (_lib.E_SHAPE, "E_LIFT_SHAPE")
+    bad_q = np.array([cf.LOCKED_PRIMES[0], 4], dtype=np.uint64)  # even modulus
+    assert code(L.praghip_lift59(0, A, A, 1, 12, 0, bad_q.ctypes.data, 2, None)) == (_lib.E_SHAPE, "E_LIFT_SHAPE")
+    assert code(L.praghip_dyadic_mac(0, A, A, A, 0, 2, 12, 2, q.ctypes.data, 2, None)) == (_lib.E_SHAPE,
+                                                                                           "E_DYADIC_SHAPE")
+    delta = np.array([q[0], 1], dtype=np.uint64)  # Delta_0 not below q_0
+    assert code(L.praghip_local_dot_scale(0, A, A, 16, 1, delta.ctypes.data, 5, q.ctypes.data, 2, A, A, None)) == (
+        _lib.E_CANONICAL, "E_LOCAL_DELTA")
+    assert code(L.praghip_local_dot_scale(0, A, A, 16, 1, delta.ctypes.data, 1 << 59, q.ctypes.data, 2, A, A,
+                                          None)) == (_lib.E_SHAPE, "E_LOCAL_SHAPE")
+    assert L.praghip_local_dot_workspace_words(3) == 3 * 256
+    descs = (_lib.GemmDesc * 2)(_lib.GemmDesc(A, A, None, A, 4, 8, 4, 8, 64), _lib.GemmDesc(A, A, None, A, 4, 8, 4, 16, 64))
+    assert code(L.praghip_share_gemm_batch(0, ctypes.cast(descs, ctypes.c_void_p), 2, None)) == (
+        _lib.E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE")
+    descs[1].w_bits, descs[1].y = 32, A + 4
+    assert code(L.praghip_share_gemm_batch(0, ctypes.cast(descs, ctypes.c_void_p), 2, None)) == (
+        _lib.E_ARGUMENT, "E_SHARE_ALIGNMENT")
