@@ -256,8 +256,8 @@ def cpu_baselines(torch, res, budget_s: float):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "qwen3", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")

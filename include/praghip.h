@@ -198,6 +198,28 @@ int praghip_local_dot_scale(int device, const uint64_t *shares, const uint64_t *
                             const uint64_t *delta, uint64_t r, const uint64_t *q, size_t primes, uint64_t *scaled,
                             uint64_t *workspace, void *stream);
 
+/* ------------------------------------------------------- HE matrix product */
+/* matrix_gpu::Matrix (matrix.hpp:9-24, matrix.cu:48-81).  create: `input` is
+ * host [blocks][2][primes][2^log_n] ciphertexts in coefficient form
+ * (canonical), kept on the device in NTT form.  evaluate: `ring` is host
+ * [blocks][2^log_n] ring-2^59 words (MATRIX_GPU_RING above 2^59 - 1); the
+ * result out[c][k][z] = INTT(sum_b NTT(ct_b[c][k]) (.) NTT(lift(ring_b))[k])
+ * is written to host [2][primes][2^log_n].  With `targets` (1..512 strictly
+ * increasing coefficient indices, evaluate_selective) the c0 coefficients
+ * outside the targets are zero.  evaluate_device: the same on device buffers,
+ * asynchronous on `stream`, full output.  Errors MATRIX_GPU_SHAPE,
+ * MATRIX_GPU_TARGET_COUNT, MATRIX_GPU_TARGET_INDEX, E_NTT_CANONICAL_REQUIRED;
+ * a device error poisons the plan. */
+typedef struct praghip_matrix_plan praghip_matrix_plan;
+int praghip_matrix_plan_create(int device, const uint64_t *q, size_t primes, uint32_t log_n, const uint64_t *input,
+                               size_t blocks, praghip_matrix_plan **plan);
+int praghip_matrix_evaluate(praghip_matrix_plan *plan, const uint64_t *ring, uint64_t *output,
+                            const uint64_t *targets, size_t count);
+int praghip_matrix_evaluate_device(praghip_matrix_plan *plan, const uint64_t *ring, uint64_t *output, void *stream);
+size_t praghip_matrix_device_bytes(const praghip_matrix_plan *plan);
+int praghip_matrix_close(praghip_matrix_plan *plan, praghip_cleanup *out);
+void praghip_matrix_destroy(praghip_matrix_plan *plan);
+
 /* ------------------------------------------------------------ weight files */
 /* The quantized_f12 int32 .npy weights (quantize_weights.py:60-64), read as
  * MappedWeights does (artifacts.hpp:31-49): memory-mapped, version 1/2, '<i4',

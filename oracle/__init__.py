@@ -276,3 +276,18 @@ def ring_sum_rows(a, cols: int, bits: int = 59) -> np.ndarray:
     out = np.empty(rows, dtype=np.uint64)
     lib().orc_ring_sum_rows(_p(a), _p(out), rows, cols, bits)
     return out
+
+
+def matrix_product(ct: np.ndarray, ring: np.ndarray, q, log_n: int, threads: int = 0) -> np.ndarray:
+    """matrix_gpu::Matrix::evaluate (matrix.cu:56-70): ct [blocks][2][P][N] coefficient form,
+    ring [blocks][N] ring-2^59 words -> INTT(sum_b NTT(ct_b) (.) NTT(lift(ring_b))) [2][P][N]."""
+    n = 1 << log_n
+    P = len(q)
+    t = Tables(q, log_n)
+    ct = _u64(ct).reshape(-1, 2 * P, n)
+    blocks = ct.shape[0]
+    w = lift59_blocks(_u64(ring).reshape(blocks, n), q, n)           # [blocks][P][N]
+    wf = ntt(w.reshape(blocks * P, n), t, threads=threads).reshape(blocks, P, n)
+    cf_ = ntt(ct.reshape(blocks * 2 * P, n), t, threads=threads).reshape(blocks, 2 * P, n)
+    acc = dyadic_mac(cf_, wf, q)                                       # [2P][N]
+    return ntt(acc, t, inverse=True, threads=threads).reshape(2, P, n)

@@ -981,3 +981,138 @@ int praghip_local_dot_scale(int device, const uint64_t* shares, const uint64_t* 
 }
 
 }  // extern "C"
+
+// ============================================================== Matrix plan
+// matrix_gpu::Matrix (matrix.hpp:9-24, matrix.cu:48-81): ciphertext blocks
+// held in NTT form; evaluate(ring) = INTT( sum_b NTT(ct_b) (.) NTT(lift(ring_b)) ).
+struct praghip_matrix_plan {
+  int device = -1;
+  unsigned log_n = 0;
+  size_t P = 0, blocks = 0;
+  std::vector<uint64_t> host_q;
+  Buffers buf;
+  NttDevice d;
+  uint64_t *input = nullptr, *ring = nullptr, *weight = nullptr, *output = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[1] = {};
+  praghip_cleanup cleanup{};
+  bool closing = false;
+  void release() { release_all(device, buf, stream, ev, 1, cleanup, closing); }
+  ~praghip_matrix_plan() { release(); }
+};
+
+namespace {
+int matrix_failure(praghip_matrix_plan* p, hipError_t e, const char* what) {
+  p->release();
+  return fail(PRAGHIP_E_DEVICE, std::string("E_MATRIX_HIP: ") + what + ": " + hipGetErrorString(e));
+}
+// lift -> NTT -> sum of products -> INTT, all on the plan's device buffers
+hipError_t matrix_run(praghip_matrix_plan* p, const uint64_t* ring_dev, uint64_t* out_dev, hipStream_t s) {
+  PrimeList pl{};
+  for (size_t i = 0; i < p->P; ++i) pl.q[i] = p->host_q[i];
+  pl.count = int(p->P);
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
+  hipError_t e = launch_lift59(ring_dev, p->weight, p->blocks, int(p->log_n), 0, pl, s);
+  if (e == hipSuccess) e = launch_ntt(false, p->weight, p->blocks * p->P, p->d, s);
+  if (e == hipSuccess)
+    e = launch_dyadic_mac(p->input, p->weight, out_dev, p->blocks, 2 * p->P, int(p->log_n), p->P, m, int(p->P), s);
+  if (e == hipSuccess) e = launch_ntt(true, out_dev, 2 * p->P, p->d, s);
+  return e;
+}
+}  // namespace
+
+extern "C" {
+
+int praghip_matrix_plan_create(int device, const uint64_t* q, size_t primes, uint32_t log_n, const uint64_t* input,
+                               size_t blocks, praghip_matrix_plan** plan) {
+  if (!plan || !q || !input) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *plan = nullptr;
+  if (log_n < 4 || log_n > 14 || primes < 1 || primes > size_t(kMaxKeyPrimes) || blocks < 1 || blocks > 4096)
+    return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_SHAPE");
+  NttHost h;
+  if (int rc = build_ntt_host(q, primes, log_n, nullptr, nullptr, nullptr, h)) return rc;
+  const size_t n = size_t(1) << log_n, in_words = blocks * 2 * primes * n;
+  std::vector<uint64_t> qv(q, q + primes);
+  if (!canonical(input, in_words, qv, log_n)) return fail(PRAGHIP_E_CANONICAL, "E_NTT_CANONICAL_REQUIRED");
+  if (int rc = check_device(device)) return rc;
+  std::unique_ptr<praghip_matrix_plan> p(new praghip_matrix_plan);
+  p->device = device;
+  p->log_n = log_n;
+  p->P = primes;
+  p->blocks = blocks;
+  p->host_q = qv;
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&p->ev[0]);
+  if (e == hipSuccess) e = upload_ntt(h, log_n, p->buf, p->d, p->stream);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->input, in_words * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->ring, blocks * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->weight, blocks * primes * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->output, 2 * primes * n * 8, true);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->input, input, in_words * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = launch_ntt(false, p->input, blocks * 2 * primes, p->d, p->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return matrix_failure(p.get(), e, "create");
+  *plan = p.release();
+  return PRAGHIP_OK;
+}
+
+int praghip_matrix_evaluate(praghip_matrix_plan* p, const uint64_t* ring, uint64_t* output, const uint64_t* targets,
+                            size_t count) {
+  if (!p || !ring || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "MATRIX_GPU_CLOSED");
+  const size_t n = size_t(1) << p->log_n, ring_words = p->blocks * n, out_words = 2 * p->P * n;
+  if (targets) {  // evaluate_selective (matrix.cu:69-73)
+    if (count == 0 || count > 512) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_TARGET_COUNT");
+    for (size_t i = 0; i < count; ++i)
+      if (targets[i] >= n || (i && targets[i] <= targets[i - 1])) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_TARGET_INDEX");
+  }
+  for (size_t i = 0; i < ring_words; ++i)
+    if (ring[i] >> 59) return fail(PRAGHIP_E_CANONICAL, "MATRIX_GPU_RING");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipMemcpyAsync(p->ring, ring, ring_words * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = matrix_run(p, p->ring, p->output, p->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(output, p->output, out_words * 8, hipMemcpyDeviceToHost, p->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) {
+    volatile uint64_t* o = output;
+    for (size_t i = 0; i < out_words; ++i) o[i] = 0;
+    return matrix_failure(p, e, "evaluate");
+  }
+  if (targets) {  // c0 keeps only the target coefficients; c1 is complete
+    std::vector<uint8_t> keep(n, 0);
+    for (size_t i = 0; i < count; ++i) keep[targets[i]] = 1;
+    for (size_t k = 0; k < p->P; ++k)
+      for (size_t z = 0; z < n; ++z)
+        if (!keep[z]) output[k * n + z] = 0;
+  }
+  return PRAGHIP_OK;
+}
+
+int praghip_matrix_evaluate_device(praghip_matrix_plan* p, const uint64_t* ring, uint64_t* output, void* stream) {
+  if (!p || !ring || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "MATRIX_GPU_CLOSED");
+  if ((reinterpret_cast<uintptr_t>(ring) | reinterpret_cast<uintptr_t>(output)) & 15)
+    return fail(PRAGHIP_E_ARGUMENT, "MATRIX_GPU_ALIGNMENT");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = matrix_run(p, ring, output, pick(stream));
+  if (e != hipSuccess) return matrix_failure(p, e, "evaluate");
+  return PRAGHIP_OK;
+}
+
+size_t praghip_matrix_device_bytes(const praghip_matrix_plan* p) { return p ? p->buf.total_bytes() : 0; }
+
+int praghip_matrix_close(praghip_matrix_plan* p, praghip_cleanup* out) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  p->release();
+  if (out) *out = p->cleanup;
+  return PRAGHIP_OK;
+}
+
+void praghip_matrix_destroy(praghip_matrix_plan* p) { delete p; }
+
+}  // extern "C"

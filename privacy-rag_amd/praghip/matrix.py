@@ -1,0 +1,71 @@
+"""HE matrix product on resident ciphertexts: mirror of matrix_gpu::Matrix
+(matrix.hpp:9-24, matrix.cu:48-81) over praghip_matrix_*."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from ._lib import Cleanup, check, lib
+from ._util import dev_ptr, host_u64, stream_handle, u64_dtypes
+
+
+class Matrix:
+    """`input`: [blocks][2][len(q)][2^log_n] ciphertexts in coefficient form
+    (canonical), kept on the device in NTT form.  evaluate(ring) with ring
+    [blocks][2^log_n] ring-2^59 words returns the coefficient-form product
+    [2][len(q)][2^log_n]; evaluate_selective keeps only the target
+    coefficients of c0 (1..512 strictly increasing indices)."""
+
+    def __init__(self, q, log_n: int, input, device: int = 0):
+        self.q = [int(x) for x in q]
+        self.log_n = log_n
+        a = host_u64(input)
+        n = 1 << log_n
+        if a.size % (2 * len(self.q) * n):
+            raise ValueError("MATRIX_GPU_SHAPE")
+        self.blocks = a.size // (2 * len(self.q) * n)
+        qa = np.asarray(self.q, dtype=np.uint64)
+        h = ctypes.c_void_p()
+        check(lib().praghip_matrix_plan_create(device, qa.ctypes.data, len(self.q), log_n, a.ctypes.data, self.blocks,
+                                               ctypes.byref(h)))
+        self._h = h
+
+    def _out(self):
+        return np.empty((2, len(self.q), 1 << self.log_n), dtype=np.uint64)
+
+    def evaluate(self, ring) -> np.ndarray:
+        r = host_u64(ring)
+        out = self._out()
+        check(lib().praghip_matrix_evaluate(self._h, r.ctypes.data, out.ctypes.data, None, 0))
+        return out
+
+    def evaluate_selective(self, ring, targets) -> np.ndarray:
+        r = host_u64(ring)
+        t = np.ascontiguousarray(targets, dtype=np.uint64)
+        out = self._out()
+        check(lib().praghip_matrix_evaluate(self._h, r.ctypes.data, out.ctypes.data, t.ctypes.data, t.size))
+        return out
+
+    def evaluate_device(self, ring, out, stream=None):
+        """ring: GPU [blocks][2^log_n] words below 2^59 (not checked); out: GPU [2][P][2^log_n]."""
+        check(lib().praghip_matrix_evaluate_device(self._h, dev_ptr(ring, u64_dtypes()), dev_ptr(out, u64_dtypes()),
+                                                   stream_handle(stream)))
+        return out
+
+    def device_bytes(self) -> int:
+        return int(lib().praghip_matrix_device_bytes(self._h))
+
+    def close(self) -> Cleanup:
+        c = Cleanup()
+        check(lib().praghip_matrix_close(self._h, ctypes.byref(c)))
+        return c
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None:
+            try:
+                lib().praghip_matrix_destroy(h)
+            except Exception:
+                pass
+            self._h = None

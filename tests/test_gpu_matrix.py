@@ -1,0 +1,69 @@
+"""GPU parity of the HE matrix product (matrix_gpu::Matrix, matrix.cu:48-81)
+against the oracle (pinned by the schoolbook negacyclic product), its
+selective variant, the device entry point and the reference's errors."""
+import numpy as np
+import pytest
+
+import closed_form as cf
+import oracle
+import praghip
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+T59 = (1 << 59) - 1
+
+
+@pytest.mark.parametrize("log_n,blocks,primes", [(14, 3, "locked"), (12, 5, "50bit"), (14, 1, "50bit")])
+def test_matrix_evaluate(gpu, log_n, blocks, primes):
+    print(f"[matrix] log_n={log_n} blocks={blocks} {primes}", flush=True)
+    n = 1 << log_n
+    q = cf.LOCKED_PRIMES[:6] if primes == "locked" else cf.primes_below(50, 2 * n, 6)
+    ct = oracle.fill_residues(blocks * 2 * 6, n, q, 300 + blocks).reshape(blocks, 2, 6, n)
+    ring = oracle.fill_u64(blocks * n, 301 + blocks).reshape(blocks, n) & np.uint64(T59)
+    ring[0, :4] = [T59, 1 << 58, 0, (1 << 58) - 1]
+    want = oracle.matrix_product(ct, ring, q, log_n)
+    m = praghip.Matrix(q, log_n, ct)
+    np.testing.assert_array_equal(m.evaluate(ring), want)
+    # a second evaluation on the same plan with other weights
+    ring2 = oracle.fill_u64(blocks * n, 302 + blocks).reshape(blocks, n) & np.uint64(T59)
+    np.testing.assert_array_equal(m.evaluate(ring2), oracle.matrix_product(ct, ring2, q, log_n))
+    # selective: c0 only at the targets, c1 complete
+    targets = np.array([0, 7, 100, n - 1], dtype=np.uint64)
+    sel = m.evaluate_selective(ring, targets)
+    mask = np.zeros(n, dtype=bool)
+    mask[targets.astype(np.int64)] = True
+    np.testing.assert_array_equal(sel[1], want[1])
+    np.testing.assert_array_equal(sel[0][:, mask], want[0][:, mask])
+    assert not sel[0][:, ~mask].any()
+    # device entry point
+    out = to_dev(np.zeros((2, 6, n), dtype=np.uint64))
+    m.evaluate_device(to_dev(ring), out)
+    import torch
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(out), want)
+    c = m.close()
+    assert c.closed and c.wipe_synchronized_bytes == c.freed_bytes > 0
+
+
+def test_matrix_errors(gpu):
+    n, q = 1 << 12, cf.primes_below(50, 1 << 13, 6)
+    ct = oracle.fill_residues(2 * 6, n, q, 5).reshape(1, 2, 6, n)
+    m = praghip.Matrix(q, 12, ct)
+    ring = np.zeros((1, n), dtype=np.uint64)
+    for bad, code in [(np.array([], dtype=np.uint64), "MATRIX_GPU_TARGET_COUNT"),
+                      (np.arange(513, dtype=np.uint64), "MATRIX_GPU_TARGET_COUNT"),
+                      (np.array([5, 5], dtype=np.uint64), "MATRIX_GPU_TARGET_INDEX"),
+                      (np.array([n], dtype=np.uint64), "MATRIX_GPU_TARGET_INDEX")]:
+        with pytest.raises(praghip.PraghipError, match=code):
+            m.evaluate_selective(ring, bad)
+    ring[0, 3] = 1 << 59
+    with pytest.raises(praghip.PraghipError, match="MATRIX_GPU_RING"):
+        m.evaluate(ring)
+    bad_ct = ct.copy()
+    bad_ct[0, 0, 0, 0] = q[0]
+    with pytest.raises(praghip.PraghipError, match="E_NTT_CANONICAL_REQUIRED"):
+        praghip.Matrix(q, 12, bad_ct)
+    m.close()
+    with pytest.raises(praghip.PraghipError, match="MATRIX_GPU_CLOSED"):
+        m.evaluate(np.zeros((1, n), dtype=np.uint64))

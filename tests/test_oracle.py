@@ -321,3 +321,30 @@ def test_lift_blocks_layouts():
                 v = int(ring5[b * 5 + 4 - z]) if z < 5 else None
                 want = 0 if v is None else (v - t if v >> 58 else v) % qk
                 assert int(out[b, k, z]) == want
+
+
+def test_matrix_product_closed_form():
+    """The HE matrix product equals sum_b ct_b(X) * m_b(X) mod (X^N + 1, q) with m_b the
+    lifted ring block (schoolbook negacyclic products in Python integers)."""
+    log_n, n = 5, 32
+    q = cf.primes_below(50, 2 * n, 2)
+    blocks = 3
+    ct = oracle.fill_residues(blocks * 2 * 2, n, q, 91).reshape(blocks, 2, 2, n)
+    ring = oracle.fill_u64(blocks * n, 92).reshape(blocks, n) & np.uint64((1 << 59) - 1)
+    ring[0, :3] = [(1 << 59) - 1, 1 << 58, 5]
+    got = oracle.matrix_product(ct, ring, q, log_n)
+    t = 1 << 59
+    for c in range(2):
+        for k, qk in enumerate(q):
+            want = [0] * n
+            for b in range(blocks):
+                m = [(int(v) - t if int(v) >> 58 else int(v)) for v in ring[b]]
+                a = [int(v) for v in ct[b, c, k]]
+                for i in range(n):
+                    for j in range(n):
+                        s = a[i] * m[j]
+                        if i + j < n:
+                            want[i + j] += s
+                        else:
+                            want[i + j - n] -= s
+            assert got[c, k].tolist() == [v % qk for v in want], (c, k)
