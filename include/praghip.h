@@ -220,6 +220,24 @@ size_t praghip_matrix_device_bytes(const praghip_matrix_plan *plan);
 int praghip_matrix_close(praghip_matrix_plan *plan, praghip_cleanup *out);
 void praghip_matrix_destroy(praghip_matrix_plan *plan);
 
+/* ------------------------------------------- public-key encryption of zero */
+/* prag::enc0_gpu::PublicZero (enc0.hpp:15-25, enc0.cu:99-114): create takes
+ * the K = data_primes + 1 key-level primes and the public key pk [2][K][N] in
+ * NTT form (host, canonical).  evaluate takes one encryption's samples
+ * [3][K][N] (u ternary, e0, e1, as residues; E_ENC0_SAMPLE_CANONICAL) and
+ * writes out[c] = ModDown(INTT(NTT(u) (.) pk_c) + e_c), host [2][L][N], then
+ * wipes every device intermediate.  evaluate_device: the same on device
+ * buffers (samples [3][K][N], out [2][L][N]), asynchronous on `stream`.
+ * Errors as Switch (E_SWITCH_SHAPE, E_SWITCH_CLOSED); a device error poisons
+ * the plan. */
+typedef struct praghip_enc0_plan praghip_enc0_plan;
+int praghip_enc0_plan_create(int device, const uint64_t *q, size_t data_primes, uint32_t log_n, const uint64_t *pk,
+                             praghip_enc0_plan **plan);
+int praghip_enc0_evaluate(praghip_enc0_plan *plan, const uint64_t *samples, uint64_t *output);
+int praghip_enc0_evaluate_device(praghip_enc0_plan *plan, const uint64_t *samples, uint64_t *output, void *stream);
+int praghip_enc0_close(praghip_enc0_plan *plan, praghip_cleanup *out);
+void praghip_enc0_destroy(praghip_enc0_plan *plan);
+
 /* ------------------------------------------------------------ weight files */
 /* The quantized_f12 int32 .npy weights (quantize_weights.py:60-64), read as
  * MappedWeights does (artifacts.hpp:31-49): memory-mapped, version 1/2, '<i4',

@@ -428,6 +428,49 @@ int orc_keyswitch(const uint64_t *in, uint64_t *out, const uint64_t *key, size_t
 }
 
 /* ------------------------------------------------------------------------ */
+/* Public-key encryption of zero at the key level, then ModDown               */
+/* (PublicZero::evaluate, enc0.cu:99-114; sequence of the CPU reference        */
+/* enc0/seal_adapter.cpp:56-61): samples [3][K][N] = u, e0, e1 as residues of  */
+/* the K = L+1 key primes; pk [2][K][N] in NTT form;                          */
+/*   P_c = INTT(NTT(u) (.) pk_c) + e_c,  out_c = ModDown_p(P_c)  [2][L][N].    */
+/* ------------------------------------------------------------------------ */
+int orc_enc0(const uint64_t *samples, const uint64_t *pk, uint64_t *out, const uint64_t *q, size_t L,
+             unsigned log_n, const uint64_t *fwd, const uint64_t *inv, const uint64_t *invn) {
+  const size_t K = L + 1, n = (size_t)1 << log_n;
+  uint64_t *u = (uint64_t *)malloc(K * n * 8), *prod = (uint64_t *)malloc(2 * K * n * 8);
+  if (!u || !prod) { free(u); free(prod); return -2; }
+  memcpy(u, samples, K * n * 8);
+  for (size_t t = 0; t < K; ++t) orc_ntt_forward(u + t * n, log_n, q[t], fwd + 2 * t * n);
+  for (size_t comp = 0; comp < 2; ++comp)
+    for (size_t t = 0; t < K; ++t) {
+      uint64_t r0, r1;
+      orc_barrett_ratio(q[t], &r0, &r1);
+      uint64_t *dst = prod + (comp * K + t) * n;
+      for (size_t k = 0; k < n; ++k) dst[k] = mul_barrett(u[t * n + k], pk[(comp * K + t) * n + k], q[t], r0, r1);
+      orc_ntt_inverse(dst, log_n, q[t], inv + 2 * t * n, invn + 2 * t);
+      const uint64_t *e = samples + ((comp + 1) * K + t) * n;
+      for (size_t k = 0; k < n; ++k) dst[k] = add_mod(dst[k], e[k], q[t]);
+    }
+  const uint64_t p = q[L], half = p >> 1;
+  for (size_t comp = 0; comp < 2; ++comp)
+    for (size_t i = 0; i < L; ++i) {
+      const uint64_t qi = q[i];
+      const uint64_t invp = orc_invmod(p % qi, qi), invp_q = orc_shoup_quotient(invp, qi);
+      const uint64_t halfmod = half % qi;
+      for (size_t k = 0; k < n; ++k) {
+        uint64_t last = prod[(comp * K + L) * n + k] + half;
+        last = last >= p ? last - p : last;
+        const uint64_t correction = sub_mod(last % qi, halfmod, qi);
+        out[(comp * L + i) * n + k] =
+            mul_shoup(sub_mod(prod[(comp * K + i) * n + k], correction, qi), invp, invp_q, qi);
+      }
+    }
+  free(u);
+  free(prod);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Party-local share GEMM (bfv_matrix.inc:177-182; same loop at :101-105 and   */
 /* :156-160): Y[b][o] = sum_j X[b][j] * W[o][j] in wrapping uint64, then the  */
 /* optional per-output left shift (exact on additive shares) and the mask to  */

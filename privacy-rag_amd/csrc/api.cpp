@@ -1116,3 +1116,138 @@ int praghip_matrix_close(praghip_matrix_plan* p, praghip_cleanup* out) {
 void praghip_matrix_destroy(praghip_matrix_plan* p) { delete p; }
 
 }  // extern "C"
+
+// ================================================================ Enc0 plan
+// prag::enc0_gpu::PublicZero (enc0.hpp:15-25, enc0.cu:99-114): the public key
+// resident in NTT form; evaluate(samples) = ModDown(INTT(NTT(u) (.) pk) + e).
+struct praghip_enc0_plan {
+  int device = -1;
+  unsigned log_n = 0;
+  size_t L = 0, K = 0;
+  std::vector<uint64_t> host_q;
+  Buffers buf;
+  NttDevice d;
+  Enc0Const kc{};
+  uint64_t *pk = nullptr, *samples = nullptr, *expanded = nullptr, *prod = nullptr, *out = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[1] = {};
+  praghip_cleanup cleanup{};
+  bool closing = false;
+  void release() { release_all(device, buf, stream, ev, 1, cleanup, closing); }
+  ~praghip_enc0_plan() { release(); }
+};
+
+namespace {
+int enc0_failure(praghip_enc0_plan* p, hipError_t e, const char* what) {
+  p->release();
+  return fail(PRAGHIP_E_DEVICE, std::string("E_ENC0_HIP: ") + what + ": " + hipGetErrorString(e));
+}
+// samples [3][K][N] on the device -> out [2][L][N]
+hipError_t enc0_run(praghip_enc0_plan* p, const uint64_t* samples, uint64_t* out, hipStream_t s) {
+  const size_t n = size_t(1) << p->log_n, K = p->K;
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < K; ++i) m[i] = barrett_of(p->host_q[i]);
+  hipError_t e = hipMemcpyAsync(p->expanded, samples, K * n * 8, hipMemcpyDeviceToDevice, s);
+  if (e == hipSuccess) e = launch_ntt(false, p->expanded, K, p->d, s);
+  // prod[c][t] = pk[c][t] (.) NTT(u)[t]: the MAC with one block, u broadcast over both components
+  if (e == hipSuccess) e = launch_dyadic_mac(p->pk, p->expanded, p->prod, 1, 2 * K, int(p->log_n), K, m, int(K), s);
+  if (e == hipSuccess) e = launch_ntt(true, p->prod, 2 * K, p->d, s);
+  if (e == hipSuccess) e = launch_enc0_moddown(p->prod, samples + K * n, out, p->kc, s);
+  return e;
+}
+}  // namespace
+
+extern "C" {
+
+int praghip_enc0_plan_create(int device, const uint64_t* q, size_t data_primes, uint32_t log_n, const uint64_t* pk,
+                             praghip_enc0_plan** plan) {
+  if (!plan || !q || !pk) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *plan = nullptr;
+  const size_t L = data_primes, K = L + 1;
+  if (log_n < 4 || log_n > 14 || L < 1 || K > size_t(kMaxKeyPrimes)) return fail(PRAGHIP_E_SHAPE, "E_SWITCH_SHAPE");
+  NttHost h;
+  if (int rc = build_ntt_host(q, K, log_n, nullptr, nullptr, nullptr, h)) return rc;
+  const size_t n = size_t(1) << log_n;
+  std::vector<uint64_t> qv(q, q + K);
+  if (!canonical(pk, 2 * K * n, qv, log_n)) return fail(PRAGHIP_E_CANONICAL, "E_NTT_CANONICAL_REQUIRED");
+  if (int rc = check_device(device)) return rc;
+  std::unique_ptr<praghip_enc0_plan> p(new praghip_enc0_plan);
+  p->device = device;
+  p->log_n = log_n;
+  p->L = L;
+  p->K = K;
+  p->host_q = qv;
+  p->kc.L = int(L);
+  p->kc.log_n = int(log_n);
+  const uint64_t sp = q[L];
+  for (size_t i = 0; i < K; ++i) p->kc.q[i] = q[i];
+  for (size_t i = 0; i < L; ++i) {
+    const uint64_t ip = invmod(sp % q[i], q[i]);
+    p->kc.invp[i] = Shoup{ip, shoup_q(ip, q[i])};
+    p->kc.half_mod[i] = (sp >> 1) % q[i];
+    p->kc.one_q[i] = shoup_q(1, q[i]);
+  }
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&p->ev[0]);
+  if (e == hipSuccess) e = upload_ntt(h, log_n, p->buf, p->d, p->stream);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->pk, 2 * K * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->samples, 3 * K * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->expanded, K * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, 2 * K * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->out, 2 * L * n * 8, true);
+  if (e == hipSuccess) e = hipMemcpyAsync(p->pk, pk, 2 * K * n * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return enc0_failure(p.get(), e, "create");
+  *plan = p.release();
+  return PRAGHIP_OK;
+}
+
+int praghip_enc0_evaluate(praghip_enc0_plan* p, const uint64_t* samples, uint64_t* output) {
+  if (!p || !samples || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  const size_t n = size_t(1) << p->log_n, words = 3 * p->K * n, out_words = 2 * p->L * n;
+  if (!canonical(samples, words, p->host_q, p->log_n)) return fail(PRAGHIP_E_CANONICAL, "E_ENC0_SAMPLE_CANONICAL");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipMemcpyAsync(p->samples, samples, words * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = enc0_run(p, p->samples, p->out, p->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(output, p->out, out_words * 8, hipMemcpyDeviceToHost, p->stream);
+  // the one-time samples and every intermediate are wiped after use (enc0.cu:112)
+  for (uint64_t* b : {p->samples, p->expanded, p->prod, p->out}) {
+    const size_t bytes = b == p->samples ? words * 8 : b == p->expanded ? p->K * n * 8
+                         : b == p->prod  ? 2 * p->K * n * 8 : out_words * 8;
+    if (e == hipSuccess) e = hipMemsetAsync(b, 0, bytes, p->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) {
+    volatile uint64_t* o = output;
+    for (size_t i = 0; i < out_words; ++i) o[i] = 0;
+    return enc0_failure(p, e, "evaluate");
+  }
+  return PRAGHIP_OK;
+}
+
+int praghip_enc0_evaluate_device(praghip_enc0_plan* p, const uint64_t* samples, uint64_t* output, void* stream) {
+  if (!p || !samples || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  if ((reinterpret_cast<uintptr_t>(samples) | reinterpret_cast<uintptr_t>(output)) & 15)
+    return fail(PRAGHIP_E_ARGUMENT, "E_ENC0_ALIGNMENT");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = enc0_run(p, samples, output, pick(stream));
+  if (e != hipSuccess) return enc0_failure(p, e, "evaluate");
+  return PRAGHIP_OK;
+}
+
+int praghip_enc0_close(praghip_enc0_plan* p, praghip_cleanup* out) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  p->release();
+  if (out) *out = p->cleanup;
+  return PRAGHIP_OK;
+}
+
+void praghip_enc0_destroy(praghip_enc0_plan* p) { delete p; }
+
+}  // extern "C"

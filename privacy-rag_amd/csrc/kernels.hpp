@@ -57,6 +57,18 @@ struct KsArgs {
   uint32_t galois_inv;   // g^-1 mod 2N (1 = identity)
 };
 
+// ModDown constants of the encryption of zero (K = L + 1 primes, p = q[L]).
+struct Enc0Const {
+  int L, log_n;
+  uint64_t q[kMaxKeyPrimes];
+  Shoup invp[kMaxKeyPrimes];      // p^-1 mod q_i
+  uint64_t half_mod[kMaxKeyPrimes];  // floor(p/2) mod q_i
+  uint64_t one_q[kMaxKeyPrimes];     // floor(2^64 / q_i)
+};
+// out [2][L][N] = ModDown(prod + noise), prod and noise [2][K][N].
+hipError_t launch_enc0_moddown(const uint64_t* prod, const uint64_t* noise, uint64_t* out, const Enc0Const& kc,
+                               hipStream_t s);
+
 // Prime list passed by value to the fill kernel.
 struct PrimeList {
   uint64_t q[kMaxKeyPrimes];

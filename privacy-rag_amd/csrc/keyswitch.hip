@@ -55,6 +55,39 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Noise add + ModDown of the public-key encryption of zero (PublicZero,
+// enc0.cu:55-63 moddown after noise_add): one thread per (component, data
+// prime, coefficient); x = prod + e for the data prime and for p, then
+// switch.cu:74-82 without the c0 term.
+__global__ void __launch_bounds__(256)
+    enc0_moddown_kernel(const uint64_t* __restrict__ prod, const uint64_t* __restrict__ noise,
+                        uint64_t* __restrict__ out, Enc0Const kc) {
+  const int L = kc.L, K = L + 1, log_n = kc.log_n;
+  const size_t n = size_t(1) << log_n, total = size_t(2 * L) << log_n;
+  const uint64_t p = kc.q[L], half = p >> 1;
+  for (size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += size_t(gridDim.x) * blockDim.x) {
+    const size_t c = idx / (size_t(L) << log_n), k = idx & (n - 1);
+    const int i = int((idx >> log_n) % unsigned(L));
+    const uint64_t qi = kc.q[i];
+    const size_t li = (c * K + i) * n + k, lp = (c * K + L) * n + k;
+    const uint64_t x = add_mod(prod[li], noise[li], qi);
+    uint64_t last = add_mod(prod[lp], noise[lp], p) + half;
+    last = last >= p ? last - p : last;
+    const uint64_t reduced = mul_shoup(last, 1, kc.one_q[i], qi);  // last mod q_i
+    const uint64_t corr = sub_mod(reduced, kc.half_mod[i], qi);
+    out[idx] = mul_shoup(sub_mod(x, corr, qi), kc.invp[i].w, kc.invp[i].wq, qi);
+  }
+}
+
+hipError_t launch_enc0_moddown(const uint64_t* prod, const uint64_t* noise, uint64_t* out, const Enc0Const& kc,
+                               hipStream_t s) {
+  const size_t total = size_t(2 * kc.L) << kc.log_n;
+  const unsigned blocks = unsigned(std::min<size_t>((total + 255) / 256, 1u << 16));
+  hipLaunchKernelGGL(enc0_moddown_kernel, dim3(blocks), dim3(256), 0, s, prod, noise, out, kc);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ fused
 // One workgroup per (ciphertext b, key prime t): ModUp of every digit to prime
 // t, its forward NTT, the key inner product and the inverse NTT of both

@@ -13,6 +13,7 @@ libpraghip.so:
 * :class:`MappedWeights` - the int32 .npy weight reader (artifacts.hpp:31-49)
 * :class:`Matrix` - the HE matrix product on resident ciphertexts
   (matrix_gpu::Matrix, matrix.hpp:9-24)
+* :class:`PublicZero` - the public-key encryption of zero (enc0.hpp:15-25)
 * :class:`Qwen3LocalGemms` - the local products of a Qwen3 forward
   (model.hpp:66-126) as one batched call
 
@@ -26,7 +27,7 @@ from .shares import (LocalShares, bfv_delta, dyadic_mac, lift59, local_dot_scale
                      ring_layout, ring_scale, ring_sum_rows, share_gemm)
 from .weights import MappedWeights  # noqa: F401
 from .qwen3 import QWEN3_0_6B, Qwen3LocalGemms, Qwen3Shape  # noqa: F401
-from .matrix import Matrix  # noqa: F401
+from .matrix import Matrix, PublicZero  # noqa: F401
 from . import synth  # noqa: F401
 
 

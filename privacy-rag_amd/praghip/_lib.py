@@ -79,6 +79,11 @@ SIGNATURES = {
     "praghip_matrix_device_bytes": (sz, [vp]),
     "praghip_matrix_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_matrix_destroy": (None, [vp]),
+    "praghip_enc0_plan_create": (i32, [i32, vp, sz, u32, vp, pp]),
+    "praghip_enc0_evaluate": (i32, [vp, vp, vp]),
+    "praghip_enc0_evaluate_device": (i32, [vp, vp, vp, vp]),
+    "praghip_enc0_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
+    "praghip_enc0_destroy": (None, [vp]),
     "praghip_weights_open": (i32, [ctypes.c_char_p, sz, sz, i32, pp]),
     "praghip_weights_shape": (i32, [vp, ctypes.POINTER(sz), ctypes.POINTER(sz)]),
     "praghip_weights_data": (vp, [vp]),

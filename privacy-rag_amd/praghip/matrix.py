@@ -69,3 +69,44 @@ class Matrix:
             except Exception:
                 pass
             self._h = None
+
+
+class PublicZero:
+    """Mirror of prag::enc0_gpu::PublicZero (enc0.hpp:15-25): the public key
+    pk [2][K][N] (NTT form, K = data primes + 1) stays on the device;
+    evaluate(samples [3][K][N]) -> ModDown(INTT(NTT(u) * pk) + e) [2][K-1][N]."""
+
+    def __init__(self, q, log_n: int, pk, device: int = 0):
+        self.q = [int(x) for x in q]
+        self.log_n = log_n
+        a = host_u64(pk)
+        qa = np.asarray(self.q, dtype=np.uint64)
+        h = ctypes.c_void_p()
+        check(lib().praghip_enc0_plan_create(device, qa.ctypes.data, len(self.q) - 1, log_n, a.ctypes.data,
+                                             ctypes.byref(h)))
+        self._h = h
+
+    def evaluate(self, samples) -> np.ndarray:
+        s = host_u64(samples)
+        out = np.empty((2, len(self.q) - 1, 1 << self.log_n), dtype=np.uint64)
+        check(lib().praghip_enc0_evaluate(self._h, s.ctypes.data, out.ctypes.data))
+        return out
+
+    def evaluate_device(self, samples, out, stream=None):
+        check(lib().praghip_enc0_evaluate_device(self._h, dev_ptr(samples, u64_dtypes()), dev_ptr(out, u64_dtypes()),
+                                                 stream_handle(stream)))
+        return out
+
+    def close(self) -> Cleanup:
+        c = Cleanup()
+        check(lib().praghip_enc0_close(self._h, ctypes.byref(c)))
+        return c
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None:
+            try:
+                lib().praghip_enc0_destroy(h)
+            except Exception:
+                pass
+            self._h = None

@@ -216,3 +216,29 @@ def share_gemm(x, w, shifts=None, mask_bits: int = 64):
             r.append(acc & mask)
         out.append(r)
     return out
+
+
+def enc0(samples, pk_ntt, q: list[int]):
+    """Big-integer statement of the public-key encryption of zero with ModDown.
+
+    samples: [3][K][n] residues of u, e0, e1 over q[0..K-1] (q[K-1] = p);
+    pk_ntt: [2][K][n] NTT-form residues.  Returns [2][K-1][n]:
+      X_c   = CRT(u) * CRT(pk_c) + CRT(e_c)  mod (X^n+1, Q*p)
+      out_c = floor((X_c + floor(p/2)) / p)  mod q_i
+    """
+    K = len(q)
+    n = len(samples[0][0])
+    p = q[K - 1]
+    QP = 1
+    for m in q:
+        QP *= m
+    psis = [minimal_psi(m, n) for m in q]
+    u = [crt([samples[0][t][k] for t in range(K)], q) for k in range(n)]
+    out = []
+    for c in range(2):
+        pc = [intt(pk_ntt[c][t], q[t], psis[t]) for t in range(K)]
+        P = [crt([pc[t][k] for t in range(K)], q) for k in range(n)]
+        e = [crt([samples[c + 1][t][k] for t in range(K)], q) for k in range(n)]
+        X = [(a + b) % QP for a, b in zip(negacyclic(u, P), e)]
+        out.append([[((x + p // 2) // p) % q[i] for x in X] for i in range(K - 1)])
+    return out

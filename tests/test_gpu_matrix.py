@@ -1,6 +1,8 @@
-"""GPU parity of the HE matrix product (matrix_gpu::Matrix, matrix.cu:48-81)
-against the oracle (pinned by the schoolbook negacyclic product), its
-selective variant, the device entry point and the reference's errors."""
+"""GPU parity of the HE matrix product (matrix_gpu::Matrix, matrix.cu:48-81) and of
+the public-key encryption of zero (PublicZero, enc0.cu:99-114) against the oracle
+(pinned by the schoolbook negacyclic product and the big-integer ModDown closed
+form): full and selective evaluation, the device entry points, the reference's
+errors and the cleanup counts."""
 import numpy as np
 import pytest
 
@@ -67,3 +69,35 @@ def test_matrix_errors(gpu):
     m.close()
     with pytest.raises(praghip.PraghipError, match="MATRIX_GPU_CLOSED"):
         m.evaluate(np.zeros((1, n), dtype=np.uint64))
+
+
+def _enc0_samples(q, n, seed):
+    u = ((oracle.fill_u64(n, seed) % np.uint64(3)).astype(np.int64) - 1)
+    e = [(oracle.fill_u64(n, seed + 1 + c) % np.uint64(41)).astype(np.int64) - 20 for c in range(2)]
+    return np.array([[np.mod(vec, m).astype(np.uint64) for m in q] for vec in [u] + e], dtype=np.uint64)
+
+
+@pytest.mark.parametrize("primes", ["locked", "50bit"])
+def test_enc0(gpu, primes):
+    """PublicZero::evaluate (enc0.cu:99-114) against the oracle (pinned by the big-integer closed form)."""
+    print(f"[enc0] {primes}", flush=True)
+    log_n, n = 14, 1 << 14
+    q = cf.LOCKED_PRIMES if primes == "locked" else cf.primes_below(50, 2 * n, 6) + cf.primes_below(60, 2 * n, 1)
+    pk = oracle.fill_residues(2 * len(q), n, q, 400).reshape(2, len(q), n)
+    z = praghip.PublicZero(q, log_n, pk)
+    for seed in (410, 420):
+        samples = _enc0_samples(q, n, seed)
+        np.testing.assert_array_equal(z.evaluate(samples), oracle.enc0(samples, pk, q, log_n))
+    out = to_dev(np.zeros((2, len(q) - 1, n), dtype=np.uint64))
+    z.evaluate_device(to_dev(samples), out)
+    import torch
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(out), oracle.enc0(samples, pk, q, log_n))
+    bad = samples.copy()
+    bad[1, 0, 5] = q[0]
+    with pytest.raises(praghip.PraghipError, match="E_ENC0_SAMPLE_CANONICAL"):
+        z.evaluate(bad)
+    c = z.close()
+    assert c.closed and c.wipe_synchronized_bytes == c.freed_bytes > 0
+    with pytest.raises(praghip.PraghipError, match="E_SWITCH_CLOSED"):
+        z.evaluate(samples)

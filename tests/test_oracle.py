@@ -348,3 +348,19 @@ def test_matrix_product_closed_form():
                         else:
                             want[i + j - n] -= s
             assert got[c, k].tolist() == [v % qk for v in want], (c, k)
+
+
+@pytest.mark.parametrize("primes", ["locked", "small"])
+def test_enc0_closed_form(primes):
+    """PublicZero: ModDown(INTT(NTT(u) * pk) + e) equals floor((u*PK + e + floor(p/2)) / p) mod q_i
+    in big integers, with ternary u and small signed noise as residues."""
+    log_n, n = 4, 16
+    q = cf.LOCKED_PRIMES if primes == "locked" else cf.primes_below(50, 2 * n, 3) + cf.primes_below(60, 2 * n, 1)
+    K = len(q)
+    u = [(int(v) % 3) - 1 for v in oracle.fill_u64(n, 51)]
+    e = [[(int(v) % 41) - 20 for v in oracle.fill_u64(n, 52 + c)] for c in range(2)]
+    samples = np.array([[[x % m for x in vec] for m in q] for vec in [u] + e], dtype=np.uint64)
+    pk = oracle.fill_residues(2 * K, n, q, 53).reshape(2, K, n)
+    got = oracle.enc0(samples, pk, q, log_n)
+    want = cf.enc0(samples.tolist(), pk.tolist(), q)
+    assert got.tolist() == want
