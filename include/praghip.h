@@ -238,6 +238,91 @@ int praghip_enc0_evaluate_device(praghip_enc0_plan *plan, const uint64_t *sample
 int praghip_enc0_close(praghip_enc0_plan *plan, praghip_cleanup *out);
 void praghip_enc0_destroy(praghip_enc0_plan *plan);
 
+/* ------------------------------------------------------ token-resident path */
+/* prag::experimental::resident::TokenWeights (resident.hpp:20-45,
+ * resident.cu:104-195, resident/seal_adapter.cpp:22-61), generalised over
+ * primes, slots, blocks and block width (the reference: 6 locked primes,
+ * <= 4 slots, 19 blocks of 8192).
+ * create: `input` is host [blocks][slots][2][primes][N] ciphertexts in
+ *   coefficient form (the adapter's flat order, seal_adapter.cpp:27-33),
+ *   canonical; the plan transforms them to NTT form on the device.  `levels`
+ *   sizes the per-slot stack (levels + 1 ciphertexts).  Errors
+ *   E_GPU_TOKEN_CONTEXT_LAYOUT (shape, non-canonical input), E_NTT_CONTEXT.
+ * evaluate (resident.cu:135-151): ring host [blocks][width] ring-2^59 words,
+ *   each |w| <= 2^20 as a signed value (E_RESIDENT_WEIGHT_SHAPE,
+ *   E_RESIDENT_WEIGHT_BOUND); output host [slots][2][primes][N], NTT form:
+ *   sum_b NTT(ct_b) (.) NTT(lift_rev(ring_b)).
+ * bind_local_shares (seal_adapter.cpp:54-60, resident.cu:126-132): host
+ *   [slots][blocks * width] words < 2^59, once (E_LOCAL_BINDING).
+ * evaluate_finished (seal_adapter.cpp:43-53): `local` host [slots] plaintext
+ *   words m < 2^59; *view receives a device pointer to [slots][2][primes][N]
+ *   coefficient-form results  x^-(width-1) (INTT(product) + Delta m x^(width-1))
+ *   valid until the next evaluation.  evaluate_local_finished
+ *   (seal_adapter.cpp:61): m from the bound shares' local dot product with the
+ *   ring words on the device (E_RESIDENT_LOCAL_SHAPE when none are bound).
+ * evaluate_device (resident.cu:152-173): device ring [blocks][width] (not
+ *   range-checked), device residues [slots][primes] (the scaled local terms)
+ *   or NULL for the bound shares, device output [slots][2][primes][N];
+ *   asynchronous on `stream`.
+ * stack_store / stack_view / download (resident.cu:174-191): a view is a
+ *   device pointer to one [2][primes][N] ciphertext; store copies it into
+ *   stack[slot][level] on `stream` (the stream that produced the view; the
+ *   reference waits on the view's ready event) (E_DEVICE_STACK_VIEW), view returns stack[slot][level]
+ *   (E_DEVICE_STACK_INDEX), download copies a view inside `finished` or the
+ *   stack to host (E_DEVICE_DOWNLOAD_VIEW).  All three wait for completion. */
+typedef struct praghip_token_plan praghip_token_plan;
+int praghip_token_plan_create(int device, const uint64_t *q, size_t primes, uint32_t log_n, size_t slots,
+                              size_t blocks, size_t width, size_t levels, const uint64_t *input,
+                              praghip_token_plan **plan);
+int praghip_token_evaluate(praghip_token_plan *plan, const uint64_t *ring, size_t words, uint64_t *output);
+int praghip_token_bind_local_shares(praghip_token_plan *plan, const uint64_t *shares, size_t words);
+int praghip_token_evaluate_finished(praghip_token_plan *plan, const uint64_t *ring, size_t words,
+                                    const uint64_t *local, const uint64_t **view);
+int praghip_token_evaluate_local_finished(praghip_token_plan *plan, const uint64_t *ring, size_t words,
+                                          const uint64_t **view);
+int praghip_token_evaluate_device(praghip_token_plan *plan, const uint64_t *ring, const uint64_t *residues,
+                                  uint64_t *output, void *stream);
+int praghip_token_stack_store(praghip_token_plan *plan, size_t slot, unsigned level, const uint64_t *view,
+                              void *stream);
+int praghip_token_stack_view(praghip_token_plan *plan, size_t slot, unsigned level, const uint64_t **view);
+int praghip_token_download(praghip_token_plan *plan, const uint64_t *view, uint64_t *output);
+int praghip_token_timing(const praghip_token_plan *plan, praghip_timing *out);
+int praghip_token_close(praghip_token_plan *plan, praghip_cleanup *out);
+void praghip_token_destroy(praghip_token_plan *plan);
+
+/* ------------------------------------------------------- acyclic packing */
+/* prag::experimental_full_switch::Packing (bfv_gpu_packing.hpp:10-45) over
+ * the keys of bfv_acyclic_pack.hpp:23-42: `keys` is host
+ * [levels][2][dnum][2][data_primes+1][N] NTT form; key [l][0] switches element
+ * 1 and key [l][1] element 2^(l+1) + 1 (the reference: 9 levels, dnum = 6;
+ * E_PACK_KEY_LEVELS for levels outside 1..log_n).  A pair at level l is
+ *   ks_{l,0}(L + x^s R) + ks_{l,1}(sigma_g(L - x^s R)),  s = N >> (l+1)
+ * (switch.cu:49-61,157-185), ciphertexts [2][data_primes][N] in coefficient
+ * form.  max_pairs bounds the pairs one batched keyswitch takes (scratch
+ * about 9.5 x 2 L N x 8 bytes per pair).
+ * pair (Packing::pair, bfv_gpu_packing.hpp:20-32): host ciphertexts,
+ *   synchronous (E_PACK_LEVEL, E_PACK_CIPHERTEXT, E_PACK_CLOSED).
+ * pair_device (Packing::pair_device, bfv_gpu_packing.hpp:33-37): `count`
+ *   pairs at one level, device [count][2][L][N] each, output not overlapping
+ *   the inputs (E_PACK_DEVICE_LEVEL, E_PACK_DEVICE_VIEW); asynchronous.
+ * tree_device: the stack merge of bfv_token_batch.inc:194-206 for `leaves`
+ *   (a power of two, <= 2^levels) consecutive coordinates at once, level by
+ *   level: `nodes` device [leaves][slots][2][L][N] is reduced in place and the
+ *   root of slot s is left in nodes[0][s].  Bit-identical to merging the
+ *   leaves one by one through the stack; every level is one batched call. */
+typedef struct praghip_pack_plan praghip_pack_plan;
+int praghip_pack_plan_create(int device, const uint64_t *q, size_t data_primes, uint32_t log_n, size_t dnum,
+                             size_t levels, const uint64_t *keys, size_t max_pairs, praghip_pack_plan **plan);
+int praghip_pack_pair(praghip_pack_plan *plan, const uint64_t *left, const uint64_t *right, unsigned level,
+                      uint64_t *output);
+int praghip_pack_pair_device(praghip_pack_plan *plan, const uint64_t *left, const uint64_t *right, size_t count,
+                             unsigned level, uint64_t *output, void *stream);
+int praghip_pack_tree_device(praghip_pack_plan *plan, uint64_t *nodes, size_t leaves, size_t slots, void *stream);
+int praghip_pack_merges(const praghip_pack_plan *plan, uint64_t *merges);
+int praghip_pack_timing(const praghip_pack_plan *plan, praghip_timing *out);
+int praghip_pack_close(praghip_pack_plan *plan, praghip_cleanup *out);
+void praghip_pack_destroy(praghip_pack_plan *plan);
+
 /* ------------------------------------------------------------ weight files */
 /* The quantized_f12 int32 .npy weights (quantize_weights.py:60-64), read as
  * MappedWeights does (artifacts.hpp:31-49): memory-mapped, version 1/2, '<i4',

@@ -307,3 +307,115 @@ def enc0(samples: np.ndarray, pk: np.ndarray, q, log_n: int) -> np.ndarray:
     rc = lib().orc_enc0(_p(s), _p(k), _p(out), _p(q), K - 1, log_n, _p(t.fwd), _p(t.inv), _p(t.invn))
     assert rc == 0
     return out
+
+
+# ------------------------------------------------- token-resident path, packing
+def _monomial_shift_limbs(a: np.ndarray, q, log_n: int, e: int) -> np.ndarray:
+    """x^e times every [..][P][N] limb (limb l over q[l % P])."""
+    n = 1 << log_n
+    q = _u64(q)
+    flat = _u64(a).reshape(-1, n)
+    out = np.empty_like(flat)
+    for l in range(flat.shape[0]):
+        lib().orc_monomial_shift(_p(flat[l]), _p(out[l]), log_n, int(q[l % len(q)]), e)
+    return out.reshape(np.shape(a))
+
+
+def token_evaluate(ct: np.ndarray, ring: np.ndarray, q, log_n: int, width: int, threads: int = 0) -> np.ndarray:
+    """TokenWeights::evaluate (resident.cu:135-151; the CPU sequence of
+    check_resident.cpp:51-59): ct [blocks][slots][2][P][N] coefficient form,
+    ring [blocks][width] -> [slots][2][P][N] NTT form,
+    sum_b NTT(ct_b) (.) NTT(lift of ring_b reversed into coefficients width-1..0)."""
+    n = 1 << log_n
+    P = len(q)
+    t = Tables(q, log_n)
+    ring = _u64(ring)
+    blocks = ring.size // width
+    ct = _u64(ct).reshape(blocks, -1, n)
+    slots = ct.shape[1] // (2 * P)
+    w = lift59_blocks(ring.reshape(blocks, width), q, n, width)            # [blocks][P][N]
+    wf = ntt(w.reshape(blocks * P, n), t, threads=threads).reshape(blocks, P, n)
+    cf_ = ntt(ct.reshape(-1, n), t, threads=threads).reshape(blocks, slots * 2 * P, n)
+    return dyadic_mac(cf_, wf, q).reshape(slots, 2, P, n)
+
+
+def token_scaled(local, q, t_bits: int = 59) -> np.ndarray:
+    """Delta-scaled local terms [slots][P] (resident/seal_adapter.cpp:43-53):
+    Delta_k m + floor((r m + t/2) / t) mod q_k, Delta_k = floor(Q/t) mod q_k,
+    r = Q mod t, Q = prod q."""
+    Q = 1
+    for x in q:
+        Q *= int(x)
+    t = 1 << t_bits
+    r = Q % t
+    out = np.empty((len(local), len(q)), dtype=np.uint64)
+    for s, m in enumerate(local):
+        m = int(m)
+        fix = (r * m + t // 2) // t
+        for k, x in enumerate(q):
+            out[s, k] = (m * ((Q // t) % int(x)) + fix) % int(x)
+    return out
+
+
+def token_finished(ct: np.ndarray, ring: np.ndarray, scaled: np.ndarray, q, log_n: int, width: int,
+                   threads: int = 0) -> np.ndarray:
+    """TokenWeights::evaluate_device (resident.cu:152-173): INTT of the
+    evaluate() product, scaled[slot][k] added at coefficient width-1 of c0,
+    then the negacyclic shift by x^-(width-1) (add_shift, resident.cu:54-59)."""
+    n = 1 << log_n
+    P = len(q)
+    acc = token_evaluate(ct, ring, q, log_n, width, threads)
+    slots = acc.shape[0]
+    coeff = ntt(acc.reshape(-1, n), Tables(q, log_n), inverse=True, threads=threads).reshape(slots, 2, P, n)
+    qa = _u64(q)
+    sc = _u64(scaled).reshape(slots, P)
+    coeff[:, 0, :, width - 1] = (coeff[:, 0, :, width - 1] + sc) % qa
+    return _monomial_shift_limbs(coeff, q, log_n, 2 * n - (width - 1))
+
+
+def pack_pair(left: np.ndarray, right: np.ndarray, level: int, keys: np.ndarray, q, dnum: int, log_n: int,
+              tables: Tables | None = None, threads: int = 0) -> np.ndarray:
+    """Acyclic packing merge (pack_pair, bfv_acyclic_pack.hpp:44-52; GPU
+    sequence switch.cu:157-185): right times x^(N >> (level+1)); the sum is
+    switched with key [level][0] (element 1), the difference with key
+    [level][1] (element 2^(level+1)+1, Galois applied first); results added.
+    left/right [2][L][N] coefficient form, keys [levels][2][dnum][2][L+1][N]."""
+    q = _u64(q)
+    L = len(q) - 1
+    n = 1 << log_n
+    dq = q[:L]
+    shifted = _monomial_shift_limbs(_u64(right).reshape(2, L, n), dq, log_n, n >> (level + 1))
+    lft = _u64(left).reshape(2, L, n)
+    qcol = dq.reshape(1, L, 1)
+    total = (lft + shifted) % qcol
+    diff = (lft + qcol - shifted) % qcol
+    k = _u64(keys)
+    kl = k.reshape(-1, 2, dnum * 2 * (L + 1) * n)[level]
+    if tables is None:
+        tables = Tables(q, log_n)
+    a = keyswitch(total[None], kl[0], q, dnum, log_n, 1, tables=tables, threads=threads)[0]
+    b = keyswitch(diff[None], kl[1], q, dnum, log_n, (2 << level) + 1, tables=tables, threads=threads)[0]
+    return (a + b) % qcol
+
+
+def pack_tree(leaves: np.ndarray, keys: np.ndarray, q, dnum: int, log_n: int, threads: int = 0) -> np.ndarray:
+    """The stack merge of bfv_token_batch.inc:194-206 over [leaves][slots][2][L][N]
+    coordinates in arrival order (leaf count a power of two): every arrival
+    merges with the stack entries below it, left = the older entry.  Returns
+    the roots [slots][2][L][N]."""
+    q = _u64(q)
+    lv = _u64(leaves)
+    m, slots = lv.shape[0], lv.shape[1]
+    tables = Tables(q, log_n)
+    roots = []
+    for s in range(slots):
+        stack = {}
+        for c in range(m):
+            cur, level = lv[c, s], 0
+            while level in stack:
+                cur = pack_pair(stack.pop(level), cur, level, keys, q, dnum, log_n, tables, threads)
+                level += 1
+            stack[level] = cur
+        assert list(stack) == [m.bit_length() - 1]
+        roots.append(stack[m.bit_length() - 1])
+    return np.stack(roots)

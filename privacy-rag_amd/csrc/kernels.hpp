@@ -49,7 +49,8 @@ struct KsArgs {
   const uint64_t* in;    // [batch][2][L][N] coefficient form
   uint64_t* out;         // [batch][2][L][N]
   const uint64_t* key;   // [dnum][2][K][N] NTT form, + b * key_stride
-  size_t key_stride;     // words between consecutive ciphertexts' keys (0 = shared)
+  size_t key_stride;     // words between consecutive keys (0 = one shared key)
+  size_t key_group = 1;  // consecutive ciphertexts that share one key: ciphertext b uses key b / key_group
   uint64_t* acc;         // scratch [acc_slots][2][N]: per-workgroup running sums
   unsigned acc_slots;
   uint64_t* prod;        // scratch [batch][2][K][N]: products in coefficient form
@@ -95,6 +96,15 @@ hipError_t launch_dyadic_mac(const uint64_t* a, const uint64_t* w, uint64_t* out
 hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,
                                   const uint64_t* delta, uint64_t r, const Barrett* m, int primes, uint64_t* scaled,
                                   uint64_t* work, hipStream_t s);
+
+// Token-resident path and packing tree (token.hip).
+hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint64_t* out, size_t slots,
+                               const PrimeList& pl, int log_n, size_t width, hipStream_t s);
+hipError_t launch_pack_prepare(const uint64_t* left, const uint64_t* right, uint64_t* sum, uint64_t* diff,
+                               size_t count, size_t first, size_t group, size_t stride, const PrimeList& pl,
+                               int log_n, size_t shift, uint32_t g, hipStream_t s);
+hipError_t launch_pack_finish(const uint64_t* a, const uint64_t* b, uint64_t* out, size_t count, const PrimeList& pl,
+                              int log_n, hipStream_t s);
 
 hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
                             hipStream_t s);

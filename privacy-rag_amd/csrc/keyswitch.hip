@@ -103,8 +103,9 @@ hipError_t launch_enc0_moddown(const uint64_t* prod, const uint64_t* noise, uint
 // transforms).  The special prime (60 bits) takes the integer path.
 struct KsFused {
   const uint64_t* in;      // [batch][2][L][N]
-  const uint64_t* key;     // [dnum][2][K][N] per ciphertext, key_stride words apart
+  const uint64_t* key;     // [dnum][2][K][N] per key, key_stride words apart
   size_t key_stride;
+  unsigned key_group;      // ciphertext b uses key b / key_group
   uint64_t* prod;          // [batch][2][K][N] coefficient form
   uint64_t* acc;           // [gridDim.x][2][N] running sums
   const KsConst* kc;
@@ -200,7 +201,7 @@ __device__ __forceinline__ void ks_item_f64(const KsFused& f, const KsConst& kc,
   const A ar(pr);
   const int K = kc.K, L = kc.L, dnum = kc.dnum;
   const uint64_t* c1 = f.in + (((size_t(b) * 2 + 1) * size_t(L)) << LOGN);
-  const uint64_t* kb = f.key + size_t(b) * f.key_stride + (size_t(t) << LOGN);
+  const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << LOGN);
   double* xl = reinterpret_cast<double*>(lds);
   uint64_t* s1 = slot;
   double acc0[kE];
@@ -255,7 +256,7 @@ __device__ __forceinline__ void ks_item_u64(const KsFused& f, const KsConst& kc,
   const A ar(pr);
   const int K = kc.K, L = kc.L, dnum = kc.dnum;
   const uint64_t* c1 = f.in + (((size_t(b) * 2 + 1) * size_t(L)) << LOGN);
-  const uint64_t* kb = f.key + size_t(b) * f.key_stride + (size_t(t) << LOGN);
+  const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << LOGN);
   uint64_t* s0 = slot;
   uint64_t* s1 = slot + (size_t(kE) * TH);
   const Barrett bar = kc.bar[t];
@@ -376,6 +377,7 @@ hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsCons
   f.in = a.in;
   f.key = a.key;
   f.key_stride = a.key_stride;
+  f.key_group = unsigned(a.key_group ? a.key_group : 1);
   f.prod = a.prod;
   f.acc = a.acc;
   f.kc = kc_dev;

@@ -14,6 +14,8 @@ libpraghip.so:
 * :class:`Matrix` - the HE matrix product on resident ciphertexts
   (matrix_gpu::Matrix, matrix.hpp:9-24)
 * :class:`PublicZero` - the public-key encryption of zero (enc0.hpp:15-25)
+* :class:`TokenWeights` and :class:`Packing` - the token-resident path
+  (resident.hpp:20-45) and the acyclic packing tree (bfv_gpu_packing.hpp:10-45)
 * :class:`Qwen3LocalGemms` - the local products of a Qwen3 forward
   (model.hpp:66-126) as one batched call
 
@@ -28,6 +30,7 @@ from .shares import (LocalShares, bfv_delta, dyadic_mac, lift59, local_dot_scale
 from .weights import MappedWeights  # noqa: F401
 from .qwen3 import QWEN3_0_6B, Qwen3LocalGemms, Qwen3Shape  # noqa: F401
 from .matrix import Matrix, PublicZero  # noqa: F401
+from .token import DeviceCipherBatch, Packing, TokenWeights, packed_target  # noqa: F401
 from . import synth  # noqa: F401
 
 

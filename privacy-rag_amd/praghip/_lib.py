@@ -84,6 +84,26 @@ SIGNATURES = {
     "praghip_enc0_evaluate_device": (i32, [vp, vp, vp, vp]),
     "praghip_enc0_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_enc0_destroy": (None, [vp]),
+    "praghip_token_plan_create": (i32, [i32, vp, sz, u32, sz, sz, sz, sz, vp, pp]),
+    "praghip_token_evaluate": (i32, [vp, vp, sz, vp]),
+    "praghip_token_bind_local_shares": (i32, [vp, vp, sz]),
+    "praghip_token_evaluate_finished": (i32, [vp, vp, sz, vp, pp]),
+    "praghip_token_evaluate_local_finished": (i32, [vp, vp, sz, pp]),
+    "praghip_token_evaluate_device": (i32, [vp, vp, vp, vp, vp]),
+    "praghip_token_stack_store": (i32, [vp, sz, ctypes.c_uint, vp, vp]),
+    "praghip_token_stack_view": (i32, [vp, sz, ctypes.c_uint, pp]),
+    "praghip_token_download": (i32, [vp, vp, vp]),
+    "praghip_token_timing": (i32, [vp, ctypes.POINTER(Timing)]),
+    "praghip_token_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
+    "praghip_token_destroy": (None, [vp]),
+    "praghip_pack_plan_create": (i32, [i32, vp, sz, u32, sz, sz, vp, sz, pp]),
+    "praghip_pack_pair": (i32, [vp, vp, vp, ctypes.c_uint, vp]),
+    "praghip_pack_pair_device": (i32, [vp, vp, vp, sz, ctypes.c_uint, vp, vp]),
+    "praghip_pack_tree_device": (i32, [vp, vp, sz, sz, vp]),
+    "praghip_pack_merges": (i32, [vp, ctypes.POINTER(u64)]),
+    "praghip_pack_timing": (i32, [vp, ctypes.POINTER(Timing)]),
+    "praghip_pack_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
+    "praghip_pack_destroy": (None, [vp]),
     "praghip_weights_open": (i32, [ctypes.c_char_p, sz, sz, i32, pp]),
     "praghip_weights_shape": (i32, [vp, ctypes.POINTER(sz), ctypes.POINTER(sz)]),
     "praghip_weights_data": (vp, [vp]),

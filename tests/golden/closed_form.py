@@ -242,3 +242,80 @@ def enc0(samples, pk_ntt, q: list[int]):
         X = [(a + b) % QP for a, b in zip(negacyclic(u, P), e)]
         out.append([[((x + p // 2) // p) % q[i] for x in X] for i in range(K - 1)])
     return out
+
+
+# --------------------------------------------- BFV encryption for invariants
+def signed_galois(a: list[int], g: int) -> list[int]:
+    """a(X) -> a(X^g) mod X^n + 1 over the integers (small signed coefficients)."""
+    big = 1 << 200
+    return [v - big if v > big // 2 else v for v in galois([v % big for v in a], g, big)]
+
+
+def switch_key(rng, q: list[int], dnum: int, s_src: list[int], s_dst: list[int]) -> list:
+    """NTT-form key [dnum][2][L+1][N] switching s_src to s_dst: digit j holds
+    (b, a) with b = -a s_dst + e + [p]_{q_t} s_src on the digit's primes
+    (the structure of acyclic_keys, bfv_acyclic_pack.hpp:31-40)."""
+    n = len(s_dst)
+    L = len(q) - 1
+    p = q[L]
+    psis = [minimal_psi(x, n) for x in q]
+    key = []
+    for j in range(dnum):
+        digit = digit_primes(L, dnum, j)
+        comp = [[], []]
+        e = [rng.randrange(-3, 4) for _ in range(n)]  # one integer error polynomial for all primes
+        for ti, qt in enumerate(q):
+            a = [rng.randrange(qt) for _ in range(n)]
+            b = [(x + y) % qt for x, y in zip(negacyclic([-v for v in a], s_dst, qt), e)]
+            if ti in digit:
+                b = [(x + (p % qt) * v) % qt for x, v in zip(b, s_src)]
+            comp[0].append(ntt(b, qt, psis[ti]))
+            comp[1].append(ntt(a, qt, psis[ti]))
+        key.append(comp)
+    return key
+
+
+def encrypt(rng, m: list[int], s: list[int], q: list[int], t: int) -> list:
+    """Symmetric BFV encryption of m mod t under s: [2][len(q)][n] residues."""
+    n = len(m)
+    Q = 1
+    for x in q:
+        Q *= x
+    a = [rng.randrange(Q) for _ in range(n)]
+    e = [rng.randrange(-3, 4) for _ in range(n)]
+    c0 = [(x + y + (Q // t) * z) % Q for x, y, z in zip(negacyclic([-v for v in a], s, Q), e, m)]
+    return [[[v % qi for v in c0] for qi in q], [[v % qi for v in a] for qi in q]]
+
+
+def decrypt(ct, s: list[int], q: list[int], t: int) -> list[int]:
+    """round(t (c0 + c1 s) / Q) mod t, c0 and c1 rebuilt by CRT."""
+    n = len(s)
+    Q = 1
+    for x in q:
+        Q *= x
+    d0 = [crt([int(ct[0][i][k]) for i in range(len(q))], q) for k in range(n)]
+    d1 = [crt([int(ct[1][i][k]) for i in range(len(q))], q) for k in range(n)]
+    phase = [(x + y) % Q for x, y in zip(d0, negacyclic(d1, s, Q))]
+    return [((t * v + Q // 2) // Q) % t for v in phase]
+
+
+def monomial(a: list[int], e: int, mod: int) -> list[int]:
+    """X^e a(X) mod (X^n + 1, mod)."""
+    n = len(a)
+    x = [0] * n
+    e %= 2 * n
+    if e < n:
+        x[e] = 1
+    else:
+        x[e - n] = mod - 1
+    return negacyclic(a, x, mod)
+
+
+def pack_plain(ml: list[int], mr: list[int], level: int, t: int) -> list[int]:
+    """Plaintext of a packing pair: m_L + X^s m_R + sigma_g(m_L - X^s m_R),
+    s = n >> (level+1), g = 2^(level+1) + 1 (bfv_acyclic_pack.hpp:44-52)."""
+    n = len(ml)
+    sh = monomial(mr, n >> (level + 1), t)
+    g = (2 << level) + 1
+    d = galois([(x - y) % t for x, y in zip(ml, sh)], g, t)
+    return [(x + y + z) % t for x, y, z in zip(ml, sh, d)]

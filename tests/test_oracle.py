@@ -177,40 +177,13 @@ def _bfv_keyswitch_roundtrip(q, dnum, g, log_n, seed):
     rng = random.Random(seed)
     n = 1 << log_n
     L = len(q) - 1
-    p = q[L]
     t = 1 << 59
-    Q = 1
-    for x in q[:L]:
-        Q *= x
     s_old, s_new = _ternary(rng, n), _ternary(rng, n)
-    psis = [cf.minimal_psi(x, n) for x in q]
-    s_rot = cf.galois([v % (1 << 200) for v in s_old], g, 1 << 200)  # exact: sign handled below
-    s_rot = [v - (1 << 200) if v > (1 << 199) else v for v in s_rot]
-    key = []
-    for j in range(dnum):
-        digit = cf.digit_primes(L, dnum, j)
-        comp = [[], []]
-        e = [rng.randrange(-3, 4) for _ in range(n)]  # one integer error polynomial for all primes
-        for ti, qt in enumerate(q):
-            a = [rng.randrange(qt) for _ in range(n)]
-            b = [(x + y) % qt for x, y in zip(cf.negacyclic([-v for v in a], s_new, qt), e)]
-            if ti in digit:
-                b = [(x + (p % qt) * v) % qt for x, v in zip(b, s_rot)]
-            comp[0].append(cf.ntt(b, qt, psis[ti]))
-            comp[1].append(cf.ntt(a, qt, psis[ti]))
-        key.append(comp)
+    key = cf.switch_key(rng, q, dnum, cf.signed_galois(s_old, g), s_new)
     m = [rng.randrange(t) for _ in range(n)]
-    a = [rng.randrange(Q) for _ in range(n)]
-    e = [rng.randrange(-3, 4) for _ in range(n)]
-    delta = Q // t
-    c0 = [(x + y + delta * z) % Q for x, y, z in zip(cf.negacyclic([-v for v in a], s_old, Q), e, m)]
-    ct = np.array([[[v % qi for v in c0] for qi in q[:L]], [[v % qi for v in a] for qi in q[:L]]], dtype=np.uint64)
+    ct = np.array(cf.encrypt(rng, m, s_old, q[:L], t), dtype=np.uint64)
     out = oracle.keyswitch(ct[None], np.array(key, dtype=np.uint64), q, dnum, log_n, g)[0]
-    d0 = [cf.crt([int(out[0][i][k]) for i in range(L)], q[:L]) for k in range(n)]
-    d1 = [cf.crt([int(out[1][i][k]) for i in range(L)], q[:L]) for k in range(n)]
-    phase = [(x + y) % Q for x, y in zip(d0, cf.negacyclic(d1, s_new, Q))]
-    dec = [((t * v + Q // 2) // Q) % t for v in phase]
-    assert dec == cf.galois(m, g, t)
+    assert cf.decrypt(out, s_new, q[:L], t) == cf.galois(m, g, t)
 
 
 @pytest.mark.parametrize("dnum,g", [(6, 1), (6, 3), (3, 1), (3, 2 * 32 - 1), (2, 5)])
@@ -364,3 +337,87 @@ def test_enc0_closed_form(primes):
     got = oracle.enc0(samples, pk, q, log_n)
     want = cf.enc0(samples.tolist(), pk.tolist(), q)
     assert got.tolist() == want
+
+
+def _signed_ring(rng, count):
+    """Ring-2^59 words of signed weights |w| <= 2^20, boundary values included
+    (check_resident.cpp:48)."""
+    edge = [0, 1, -1, 1 << 20, -(1 << 20), (1 << 20) - 1, -((1 << 20) - 1)]
+    vals = [edge[i] if i < len(edge) else rng.randint(-(1 << 20), 1 << 20) for i in range(count)]
+    rng.shuffle(vals)
+    return vals, np.array([v & ((1 << 59) - 1) for v in vals], dtype=np.uint64)
+
+
+@pytest.mark.parametrize("bits,width", [(60, 8), (60, 32), (50, 8), (50, 1)])
+def test_token_closed_form(bits, width):
+    """finished[s][c] = sum_b (sum_j w_b[j] X^-j) ct_b[s][c] + [c = 0] round(Q m_s / 2^59):
+    the resident path's reverse-lift, product, add_shift chain against the
+    direct negacyclic statement; evaluate() against the product with the
+    reversed weights; the scaled term against the exact rounded division."""
+    log_n, P, blocks, slots = 5, 2, 3, 2
+    n = 1 << log_n
+    q = cf.LOCKED_PRIMES[:P] if bits == 60 else cf.primes_below(50, n, P)
+    rng = random.Random(bits * 100 + width)
+    ct = np.array([[[[[rng.randrange(x) for _ in range(n)] for x in q] for _ in range(2)] for _ in range(slots)]
+                   for _ in range(blocks)], dtype=np.uint64)
+    signed, ring = _signed_ring(rng, blocks * width)
+    local = [rng.randrange(1 << 59) for _ in range(slots - 1)] + [(1 << 59) - 1]
+    Q = q[0] * q[1]
+    scaled = oracle.token_scaled(local, q)
+    for s, m in enumerate(local):
+        assert [int(v) for v in scaled[s]] == [((2 * Q * m + (1 << 59)) // (1 << 60)) % x for x in q]
+    got = oracle.token_finished(ct, ring, scaled, q, log_n, width)
+    ev = oracle.ntt(oracle.token_evaluate(ct, ring, q, log_n, width).reshape(-1, n), oracle.Tables(q, log_n),
+                    inverse=True).reshape(slots, 2, P, n)
+    for s in range(slots):
+        for c in range(2):
+            for k, x in enumerate(q):
+                want, want_ev = [0] * n, [0] * n
+                for b in range(blocks):
+                    w = signed[b * width:(b + 1) * width]
+                    inv = [0] * n            # sum_j w[j] X^-j, X^-j = -X^(n-j)
+                    rev = [0] * n            # sum_j w[j] X^(width-1-j)
+                    for j, v in enumerate(w):
+                        if j == 0:
+                            inv[0] += v
+                        else:
+                            inv[n - j] -= v
+                        rev[width - 1 - j] += v
+                    a = [int(v) for v in ct[b, s, c, k]]
+                    want = [(u + v) % x for u, v in zip(want, cf.negacyclic(a, inv, x))]
+                    want_ev = [(u + v) % x for u, v in zip(want_ev, cf.negacyclic(a, rev, x))]
+                if c == 0:
+                    want[0] = (want[0] + int(scaled[s, k])) % x
+                assert [int(v) for v in got[s, c, k]] == want, (s, c, k)
+                assert [int(v) for v in ev[s, c, k]] == want_ev, (s, c, k)
+
+
+@pytest.mark.parametrize("dnum", [6, 3])
+def test_pack_pair_and_tree_decrypt(dnum):
+    """Packing invariant with the acyclic key chain s_0 -> s_1 -> s_2 (level l's
+    keys switch s_l and sigma_g(s_l) to s_(l+1), bfv_acyclic_pack.hpp:23-42):
+    pair(L, R, l) decrypts under s_(l+1) to m_L + X^s m_R + sigma_g(m_L - X^s m_R),
+    and a tree over four leaves per slot decrypts under s_2 to that map applied
+    level by level."""
+    log_n, levels = 5, 2
+    n = 1 << log_n
+    q = cf.LOCKED_PRIMES
+    L = len(q) - 1
+    t = 1 << 59
+    rng = random.Random(dnum)
+    sec = [_ternary(rng, n) for _ in range(levels + 1)]
+    keys = []
+    for lv in range(levels):
+        g = (2 << lv) + 1
+        keys.append([cf.switch_key(rng, q, dnum, sec[lv], sec[lv + 1]),
+                     cf.switch_key(rng, q, dnum, cf.signed_galois(sec[lv], g), sec[lv + 1])])
+    keys = np.array(keys, dtype=np.uint64)
+    slots = 2
+    ms = [[[rng.randrange(t) for _ in range(n)] for _ in range(slots)] for _ in range(4)]
+    cts = np.array([[cf.encrypt(rng, m, sec[0], q[:L], t) for m in row] for row in ms], dtype=np.uint64)
+    out = oracle.pack_pair(cts[0, 0], cts[1, 0], 0, keys, q, dnum, log_n)
+    assert cf.decrypt(out, sec[1], q[:L], t) == cf.pack_plain(ms[0][0], ms[1][0], 0, t)
+    roots = oracle.pack_tree(cts, keys, q, dnum, log_n)
+    for s in range(slots):
+        want = cf.pack_plain(cf.pack_plain(ms[0][s], ms[1][s], 0, t), cf.pack_plain(ms[2][s], ms[3][s], 0, t), 1, t)
+        assert cf.decrypt(roots[s], sec[2], q[:L], t) == want
