@@ -175,6 +175,55 @@ def bench_qwen3(torch, praghip, steps, warmup):
             "_model": m}
 
 
+def bench_token(torch, praghip, steps, warmup, slots=4):
+    """One 512-coordinate tile of the token-resident path at the reference's
+    shape (bfv_token_batch.inc:176-215 with the locked context: N=16384, six
+    60-bit primes + special, 19 blocks of 8192 per slot, 4 slots, bound local
+    shares): every coordinate's weight column evaluated to a finished batch
+    (lift, NTT, 19-block product, INTT, Delta term, shift), then the 9-level
+    acyclic packing tree over the tile (511 merges per slot, 2 keyswitches each,
+    dnum=6), level by level in batched launches."""
+    from praghip import params, synth
+    q = list(params.LOCKED_PRIMES)
+    P, blocks, width, coords, levels = 6, 19, 8192, 512, 9
+    ct_words = 2 * P * N
+    inputs = torch.empty(blocks * slots * ct_words, dtype=torch.int64, device="cuda")
+    synth.fill_residues(inputs, q[:P], LOG_N, 0x5052414700000006)
+    tw = praghip.TokenWeights(q[:P], LOG_N, inputs.cpu().numpy().reshape(blocks, slots, 2, P, N), width, levels)
+    del inputs
+    shares = torch.empty(slots * blocks * width, dtype=torch.int64, device="cuda")
+    synth.fill_u64(shares, 0x5052414700000106)
+    tw.bind_local_shares((shares & ((1 << 59) - 1)).cpu().numpy())
+    del shares
+    keys = torch.empty(levels * 2 * P * 2 * (P + 1) * N, dtype=torch.int64, device="cuda")
+    synth.fill_residues(keys, q, LOG_N, 0x5052414700000206)
+    pk = praghip.Packing(q, LOG_N, keys.cpu().numpy(), dnum=P, max_pairs=512)
+    del keys
+    rings = torch.empty(coords * blocks * width, dtype=torch.int64, device="cuda")
+    synth.fill_u64(rings, 0x5052414700000306)
+    rings = ((rings & ((1 << 21) - 1)) - (1 << 20)) & ((1 << 59) - 1)  # signed |w| <= 2^20 as ring words
+    rings = rings.view(coords, blocks * width)
+    nodes = torch.empty((coords, slots * ct_words), dtype=torch.int64, device="cuda")
+
+    def evaluate_all():
+        for c in range(coords):
+            tw.evaluate_device(rings[c], nodes[c])
+
+    def step():
+        evaluate_all()
+        pk.tree_device(nodes, slots=slots)
+
+    ms = Timer(torch).run(step, steps, warmup)
+    ms_eval = Timer(torch).run(evaluate_all, steps, 1)
+    merges = (coords - 1) * slots
+    return {"slots": slots, "coordinates": coords, "blocks": blocks, "block_width": width, "levels": levels,
+            "ms_per_step": ms, "ms_per_tile": ms, "coordinates_per_s": coords / (ms * 1e-3),
+            "evaluate_ms_per_tile": ms_eval, "pack_ms_per_tile": ms - ms_eval,
+            "merges_per_tile": merges, "pack_keyswitch_per_s": 2 * merges / ((ms - ms_eval) * 1e-3),
+            "device_bytes": int(tw.timing().device_bytes + pk.timing().device_bytes),
+            "_plans": (tw, pk, rings, nodes)}
+
+
 def bench_copy(torch, steps, warmup):
     """Plain device copy of 384 MiB (the bytes one NTT launch reads, and again writes):
     the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -258,7 +307,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "qwen3", "copy"], default="all")
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "qwen3", "token", "copy"],
+                    default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
     args = ap.parse_args()
@@ -303,6 +353,14 @@ def main() -> int:
                 sample.append((x[:16].cpu(), w.cpu(), None if sh is None else sh.cpu(), y[:16].cpu()))
             res["qwen3"]["_sample"] = sample
             del m
+    if args.only in ("all", "token"):
+        log("token-resident tile: 512 coordinates x 4 slots, 9-level packing tree ...")
+        tsteps = max(1, min(args.steps, 3))
+        res["token"] = bench_token(torch, praghip, tsteps, 1)
+        log(f"token tile {res['token']['ms_per_tile']:.1f} ms ({res['token']['coordinates_per_s']:.4g} coordinates/s, "
+            f"evaluate {res['token']['evaluate_ms_per_tile']:.1f} ms)")
+        res["token"]["steps"] = tsteps
+        res["token"].pop("_plans")
     cpu = {}
     if not args.no_cpu and args.only == "all":
         log("oracle CPU baselines ...")
@@ -312,11 +370,13 @@ def main() -> int:
     def clean(d):
         return {k: v for k, v in d.items() if not k.startswith("_")}
 
-    key = next(k for k in ("ntt", "keyswitch", "gemm", "qwen3") if k in res)
+    key = next(k for k in ("ntt", "keyswitch", "gemm", "qwen3", "token") if k in res)
     primary = res[key]
     value = {"ntt": lambda r: r["ntt_per_s"], "keyswitch": lambda r: r["keyswitch_per_s"],
-             "gemm": lambda r: r["tops"], "qwen3": lambda r: r["tops"]}[key](primary)
-    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "gemm": "TOPS", "qwen3": "TOPS"}[key]
+             "gemm": lambda r: r["tops"], "qwen3": lambda r: r["tops"],
+             "token": lambda r: r["coordinates_per_s"]}[key](primary)
+    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "gemm": "TOPS", "qwen3": "TOPS",
+            "token": "coordinates/s"}[key]
     line = {
         "metric": METRIC,
         "value": value,
@@ -335,9 +395,10 @@ def main() -> int:
                    "256 ciphertexts x 2 polynomials = 3072 limbs",
             "keyswitch": "keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
             "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64",
-            "qwen3": "Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens"}[key],
+            "qwen3": "Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens",
+            "token": "token-resident tile, 512 coordinates x 4 slots, 19 blocks of 8192, 9-level packing"}[key],
             "N": N, "parallelism": "single GPU"},
-        "roofline": primary["roofline"],
+        "roofline": primary.get("roofline"),
         "cpu_baseline": cpu.get(key),
         "extra": {k: clean(v) for k, v in res.items() if k != key},
     }

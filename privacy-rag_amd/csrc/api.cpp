@@ -538,6 +538,7 @@ struct praghip_switch_plan {
   KsConst kc{};
   KsConst* kc_dev = nullptr;
   uint64_t *key = nullptr, *acc = nullptr, *prod = nullptr, *in = nullptr, *out = nullptr;
+  unsigned* queue = nullptr;
   unsigned acc_slots = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev[4] = {};
@@ -647,6 +648,8 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
     p->acc_slots = ks_acc_slots(int(log_n));
     e = p->acc_slots ? p->buf.alloc((void**)&p->acc, size_t(p->acc_slots) * 2 * n * 8, true) : hipErrorInvalidValue;
   }
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
+  if (e == hipSuccess) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, max_batch * 2 * K * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->in, 2 * L * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->out, 2 * L * n * 8, true);
@@ -672,6 +675,7 @@ static hipError_t keyswitch_chunks(praghip_switch_plan* p, const uint64_t* in, u
     a.acc_slots = p->acc_slots;
     a.prod = p->prod;
     a.galois_inv = ginv;
+    a.queue = p->queue;
     const hipError_t e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);
     if (e != hipSuccess) return e;
   }
@@ -1270,6 +1274,7 @@ struct praghip_pack_plan {
   KsConst* kc_dev = nullptr;
   uint64_t *keys = nullptr, *work = nullptr, *ksout = nullptr, *prod = nullptr, *acc = nullptr;
   uint64_t *host_in = nullptr, *host_out = nullptr;
+  unsigned* queue = nullptr;
   unsigned acc_slots = 0;
   size_t merges = 0;
   hipStream_t stream = nullptr;
@@ -1317,6 +1322,7 @@ hipError_t pack_run(praghip_pack_plan* p, const uint64_t* left, const uint64_t* 
     a.prod = p->prod;
     a.batch = 2 * c;
     a.galois_inv = 1;  // the Galois map is applied by the prepare kernel
+    a.queue = p->queue;
     e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);
     if (e == hipSuccess) e = launch_pack_finish(p->ksout, p->ksout + c * ct, out + c0 * ct, c, pl, int(p->log_n), s);
   }
@@ -1366,6 +1372,8 @@ int praghip_pack_plan_create(int device, const uint64_t* q, size_t data_primes, 
     p->acc_slots = ks_acc_slots(int(log_n));
     e = p->acc_slots ? p->buf.alloc((void**)&p->acc, size_t(p->acc_slots) * 2 * n * 8, true) : hipErrorInvalidValue;
   }
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
+  if (e == hipSuccess) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->work, 2 * max_pairs * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->ksout, 2 * max_pairs * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, 2 * max_pairs * 2 * K * n * 8, true);

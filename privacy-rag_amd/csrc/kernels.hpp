@@ -56,7 +56,12 @@ struct KsArgs {
   uint64_t* prod;        // scratch [batch][2][K][N]: products in coefficient form
   size_t batch;
   uint32_t galois_inv;   // g^-1 mod 2N (1 = identity)
+  unsigned* queue;       // scratch [kQueueWords], zero before the first launch (the kernel leaves it zero)
 };
+// Work-queue counters of the fused keyswitch: one ticket per XCD group, then
+// the count of finished workgroups.
+constexpr unsigned kQueueGroups = 8;
+constexpr unsigned kQueueWords = 16;
 
 // ModDown constants of the encryption of zero (K = L + 1 primes, p = q[L]).
 struct Enc0Const {

@@ -119,6 +119,7 @@ struct KsFused {
   uint32_t ginv;
   int data_f64;  // every data prime is below 2^50
   int xcd;       // items of one ciphertext on one XCD (batch and grid multiples of 8)
+  unsigned* queue;  // [kQueueWords]: per-group tickets, then the finished-workgroup count; zero between launches
 };
 
 __device__ __forceinline__ uint64_t as_u64(double x) { return (uint64_t)__double_as_longlong(x); }
@@ -297,27 +298,55 @@ __device__ __forceinline__ void ks_item_u64(const KsFused& f, const KsConst& kc,
   }
 }
 
+// Items are handed out from a ticket counter, so a workgroup that finishes
+// early takes the next item instead of following a fixed stride.  With the
+// float path the special-prime item (integer path) costs about 1.7 float
+// items; those are issued first, so the long items start in the first wave of
+// the grid and the short ones fill in behind them (longest first).  With xcd
+// set, workgroup w (on XCD w % 8) serves only ciphertexts b == w (mod 8) from
+// queue w % 8, keeping the K items that re-read a ciphertext's c1 on one L2.
+// The last workgroup to leave zeroes the counters for the next launch.  Every
+// workgroup exits once its ticket passes the item count, so the loop always
+// ends.
 template <int LOGN>
 __global__ void __launch_bounds__(ntt_threads<LOGN>()) ks_fused_kernel(KsFused f) {
   __shared__ __attribute__((aligned(16))) uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
+  __shared__ unsigned ticket;
   const KsConst& kc = *f.kc;
   const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
   uint64_t* slot = f.acc + (size_t(blockIdx.x) * 2 * kE * ntt_threads<LOGN>());
-  for (unsigned v = blockIdx.x; v < f.items; v += gridDim.x) {
-    unsigned b, t;
-    if (f.xcd) {  // item v runs on XCD v % 8: keep a ciphertext's K items there
-      const unsigned u = v >> 3;
-      b = (v & 7) + 8 * (u / K);
-      t = u % K;
+  const unsigned groups = f.xcd ? 8u : 1u, g = f.xcd ? (blockIdx.x & 7u) : 0u;
+  const unsigned cts = f.batch / groups;  // ciphertexts of this group: b = i * groups + g
+  const unsigned count = cts * K;
+  const bool split = f.data_f64 && K > 1;  // integer-path items (t = L) first
+  for (;;) {
+    __syncthreads();  // the previous item's LDS use and ticket reads are over
+    if (threadIdx.x == 0) ticket = atomicAdd(f.queue + g, 1u);
+    __syncthreads();
+    const unsigned k = ticket;
+    if (k >= count) break;
+    unsigned i, t;
+    if (!split) {
+      i = k / K;
+      t = k % K;
+    } else if (k < cts) {
+      i = k;
+      t = L;
     } else {
-      b = v / K;
-      t = v % K;
+      i = (k - cts) / L;
+      t = (k - cts) % L;
     }
-    __syncthreads();  // the previous item's LDS use is over
+    const unsigned b = i * groups + g;
     if (f.data_f64 && t < L)
       ks_item_f64<LOGN>(f, kc, b, int(t), lds, slot);
     else
       ks_item_u64<LOGN>(f, kc, b, int(t), lds, slot);
+  }
+  if (threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(f.queue + kQueueGroups, 1u) == gridDim.x - 1) {
+      for (unsigned q = 0; q <= kQueueGroups; ++q) atomicExch(f.queue + q, 0u);
+    }
   }
 }
 
@@ -364,7 +393,7 @@ unsigned ks_acc_slots(int log_n) {
 template <int LOGN>
 static hipError_t launch_fused_n(KsFused f, hipStream_t s) {
   const unsigned blocks = std::min(f.items, std::min(fused_grid<LOGN>(), f.acc_slots));
-  f.xcd = (f.batch % 8 == 0 && blocks % 8 == 0) ? 1 : 0;
+  f.xcd = (f.batch % kQueueGroups == 0 && blocks % kQueueGroups == 0) ? 1 : 0;
   hipLaunchKernelGGL((ks_fused_kernel<LOGN>), dim3(blocks), dim3(ntt_threads<LOGN>()), 0, s, f);
   return hipGetLastError();
 }
@@ -390,6 +419,7 @@ hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsCons
   f.items = unsigned(a.batch * kc.K);
   f.acc_slots = a.acc_slots;
   f.ginv = a.galois_inv;
+  f.queue = a.queue;
   f.data_f64 = 1;
   for (int i = 0; i < kc.L; ++i) f.data_f64 &= kc.q[i] < (1ull << 50) ? 1 : 0;
   f.xcd = 0;
