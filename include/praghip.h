@@ -115,9 +115,10 @@ int praghip_switch_plan_create(int device, const uint64_t *q, size_t data_primes
  * [2][L][N] coefficient-form ciphertext -> Galois(element) + keyswitch -> host
  * [2][L][N]. */
 int praghip_switch_apply(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output);
-/* Batched device keyswitch: in/out device [batch][2][L][N]; keys device
- * [dnum][2][L+1][N] per ciphertext at key_stride words apart (0: one shared
- * key; NULL keys: the plan's key).  galois_elt odd, < 2N (1 = plain switch). */
+/* Batched device keyswitch: in/out device [batch][2][L][N] (8-byte aligned);
+ * keys device [dnum][2][L+1][N] per ciphertext at key_stride words apart (0:
+ * one shared key; NULL keys: the plan's key), 16-byte aligned with an even
+ * key_stride (E_SWITCH_ALIGNMENT).  galois_elt odd, < 2N (1 = plain switch). */
 int praghip_keyswitch(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output, size_t batch,
                       const uint64_t *keys, size_t key_stride, uint32_t galois_elt, void *stream);
 int praghip_switch_sync(praghip_switch_plan *plan);

@@ -688,9 +688,9 @@ int praghip_keyswitch(praghip_switch_plan* p, const uint64_t* input, uint64_t* o
   if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
   if (batch && (!input || !output)) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (input == output && batch) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ALIAS");
-  if ((reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(output) |
-       reinterpret_cast<uintptr_t>(keys)) & 7)
-    return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ALIGNMENT: 8-byte aligned buffers");
+  if ((reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(output)) & 7 ||
+      (reinterpret_cast<uintptr_t>(keys) & 15) || (key_stride & 1))
+    return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ALIGNMENT: 8-byte aligned ciphertexts, 16-byte aligned keys, even key_stride");
   if (!keys && !p->key) return fail(PRAGHIP_E_STATE, "E_SWITCH_NO_KEY");
   uint32_t ginv = 1;
   if (!galois_inverse(galois_elt, p->log_n, ginv)) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ELEMENT");

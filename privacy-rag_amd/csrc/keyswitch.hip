@@ -217,15 +217,24 @@ __device__ __forceinline__ void ks_item_f64(const KsFused& f, const KsConst& kc,
     const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << LOGN);
     const uint64_t* k1 = k0 + (size_t(K) << LOGN);
 #pragma unroll
-    for (int r = 0; r < kE; ++r) {
-      const unsigned pos = fwd_out_index<LOGN>(th, r), si = unsigned(r) * TH + th;
-      // |e| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
-      const double p0 = ar.mul(e[r], ArF64::from_u64(k0[pos]));
-      double p1 = ar.mul(e[r], ArF64::from_u64(k1[pos]));
-      acc0[r] = reduce_f64(j ? acc0[r] + p0 : p0, ar.q, ar.qinv);
-      if (j) p1 += as_f64(s1[si]);
-      s1[si] = as_u64(reduce_f64(p1, ar.q, ar.qinv));
-      if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    for (int r = 0; r < kE; r += 2) {
+      // registers r and r + 1 sit at adjacent positions after the last
+      // forward pass: one 16-byte load per key limb
+      const unsigned pos = fwd_out_index<LOGN>(th, r);
+      const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+      const ulonglong2 kb = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int rr = r + h;
+        const unsigned si = unsigned(rr) * TH + th;
+        // |e| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
+        const double p0 = ar.mul(e[rr], ArF64::from_u64(h ? ka.y : ka.x));
+        double p1 = ar.mul(e[rr], ArF64::from_u64(h ? kb.y : kb.x));
+        acc0[rr] = reduce_f64(j ? acc0[rr] + p0 : p0, ar.q, ar.qinv);
+        if (j) p1 += as_f64(s1[si]);
+        s1[si] = as_u64(reduce_f64(p1, ar.q, ar.qinv));
+      }
+      if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
     }
   }
   uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << LOGN);

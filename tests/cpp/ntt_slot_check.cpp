@@ -6,7 +6,8 @@
 //   - when uniform_groups() holds, the twiddle group (bits above the gap bits)
 //     is the same for all lanes of a wave;
 //   - consecutive passes with equal wave bits give each wave the same
-//     coefficients (their exchange stays inside the wave).
+//     coefficients (their exchange stays inside the wave);
+//   - the forward output registers pair up at adjacent positions.
 #include <cstdio>
 #include <vector>
 
@@ -55,7 +56,14 @@ int check_pass() {
 
 template <int LOGN>
 int check_size() {
-  return check_pass<LOGN, false, 0>() + check_pass<LOGN, true, 0>();
+  // after the last forward pass registers 2k and 2k + 1 sit at adjacent,
+  // 16-byte aligned positions (the keyswitch loads its keys in pairs)
+  using Last = PassMap<LOGN, false, Passes<LOGN>::NP - 1>;
+  int bad = 0;
+  for (unsigned t = 0; t < (1u << LOGN) >> kLogE; ++t)
+    for (int j = 0; j < kE; j += 2) bad += (Last::elem(t, j) & 1) || Last::elem(t, j + 1) != Last::elem(t, j) + 1;
+  if (bad) printf("LOGN=%d: %d unpaired forward outputs\n", LOGN, bad);
+  return bad + check_pass<LOGN, false, 0>() + check_pass<LOGN, true, 0>();
 }
 
 int main() {

@@ -92,6 +92,16 @@ def test_switch_errors_and_cleanup(gpu):
     with pytest.raises(praghip.PraghipError) as e:
         sw.keyswitch(tin, tout, galois=2)
     assert "E_SWITCH_ELEMENT" in e.value.text
+    # keys are read in 16-byte pairs: an 8-byte offset or an odd stride is refused
+    tk = to_dev(np.concatenate([np.zeros(2, dtype=np.uint64), key.reshape(-1)]))
+    for keys, stride in [(tk[1:1 + key.size], 0), (tk[2:], 1)]:
+        with pytest.raises(praghip.PraghipError) as e:
+            sw.keyswitch(tin, tout, keys=keys, key_stride=stride)
+        assert "E_SWITCH_ALIGNMENT" in e.value.text
+    sw.keyswitch(tin, tout, keys=tk[2:], key_stride=0)
+    import torch
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(tout), sw.apply(ct))
     t = sw.timing()
     c = sw.close()
     assert c.closed and c.first_hip_error == 0
