@@ -180,7 +180,8 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
     shape (bfv_token_batch.inc:176-215 with the locked context: N=16384, six
     60-bit primes + special, 19 blocks of 8192 per slot, 4 slots, bound local
     shares): every coordinate's weight column evaluated to a finished batch
-    (lift, NTT, 19-block product, INTT, Delta term, shift), then the 9-level
+    (lift, NTT, 19-block product, INTT, Delta term, shift; 16 columns per
+    batched call), then the 9-level
     acyclic packing tree over the tile (511 merges per slot, 2 keyswitches each,
     dnum=6), level by level in batched launches."""
     from praghip import params, synth
@@ -204,10 +205,12 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
     rings = ((rings & ((1 << 21) - 1)) - (1 << 20)) & ((1 << 59) - 1)  # signed |w| <= 2^20 as ring words
     rings = rings.view(coords, blocks * width)
     nodes = torch.empty((coords, slots * ct_words), dtype=torch.int64, device="cuda")
+    chunk = 16
+    tw.reserve(chunk)
 
     def evaluate_all():
-        for c in range(coords):
-            tw.evaluate_device(rings[c], nodes[c])
+        for c in range(0, coords, chunk):
+            tw.evaluate_device_batch(rings[c:c + chunk], nodes[c:c + chunk])
 
     def step():
         evaluate_all()

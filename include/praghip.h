@@ -283,6 +283,19 @@ int praghip_token_evaluate_local_finished(praghip_token_plan *plan, const uint64
                                           const uint64_t **view);
 int praghip_token_evaluate_device(praghip_token_plan *plan, const uint64_t *ring, const uint64_t *residues,
                                   uint64_t *output, void *stream);
+/* Batched evaluate_device: the per-coordinate calls of the token loop
+ * (bfv_token_batch.inc:186-192, one resident.cu:152-173 evaluation each) for
+ * `coords` columns at once,
+ * rings device [coords][blocks][width], residues device
+ * [coords][slots][primes] or NULL (bound shares), output device
+ * [coords][slots][2][primes][N]; each column's result equals its
+ * evaluate_device result.  The resident inputs are read once per group of
+ * columns instead of once per column.  reserve(coords) allocates the batch
+ * scratch once (E_RESIDENT_BATCH_RESERVED when asked to grow it later);
+ * evaluate_device_batch takes coords <= the reserved count (E_RESIDENT_BATCH). */
+int praghip_token_reserve(praghip_token_plan *plan, size_t coords);
+int praghip_token_evaluate_device_batch(praghip_token_plan *plan, const uint64_t *rings, const uint64_t *residues,
+                                        uint64_t *output, size_t coords, void *stream);
 int praghip_token_stack_store(praghip_token_plan *plan, size_t slot, unsigned level, const uint64_t *view,
                               void *stream);
 int praghip_token_stack_view(praghip_token_plan *plan, size_t slot, unsigned level, const uint64_t **view);

@@ -1303,13 +1303,14 @@ hipError_t pack_run(praghip_pack_plan* p, const uint64_t* left, const uint64_t* 
   for (size_t i = 0; i < p->L; ++i) pl.q[i] = p->host_q[i];
   pl.count = int(p->L);
   const size_t shift = n >> (level + 1);
-  const uint32_t g = (2u << level) + 1;
+  uint32_t ginv = 1;
+  galois_inverse((2u << level) + 1, p->log_n, ginv);  // g = 2^(level+1) + 1 is odd and < 2N
   hipError_t e = hipSuccess;
   for (size_t c0 = 0; c0 < count && e == hipSuccess; c0 += p->max_pairs) {
     const size_t c = std::min(p->max_pairs, count - c0);
     uint64_t* sum = p->work;
     uint64_t* diff = p->work + c * ct;
-    e = launch_pack_prepare(left, right, sum, diff, c, c0, group, stride, pl, int(p->log_n), shift, g, s);
+    e = launch_pack_prepare(left, right, sum, diff, c, c0, group, stride, pl, int(p->log_n), shift, ginv, s);
     if (e != hipSuccess) break;
     KsArgs a;
     a.in = p->work;
@@ -1503,6 +1504,10 @@ struct praghip_token_plan {
   NttDevice d;
   uint64_t *input = nullptr, *ring = nullptr, *weight = nullptr, *output = nullptr, *finished = nullptr;
   uint64_t *scaled = nullptr, *stack = nullptr, *local_shares = nullptr, *local_partial = nullptr;
+  // batch scratch (praghip_token_reserve): [cap][blocks][P][N] weights, [cap][slots][2][P][N] products,
+  // [cap][slots][P] scaled terms, [cap * slots][kLocalTiles] local-dot partials
+  size_t batch_cap = 0;
+  uint64_t *bweight = nullptr, *boutput = nullptr, *bscaled = nullptr, *bpartial = nullptr;
   hipStream_t stream = nullptr;
   hipEvent_t ev[4] = {};
   praghip_timing timing{};
@@ -1760,6 +1765,59 @@ int praghip_token_evaluate_local_finished(praghip_token_plan* p, const uint64_t*
   if (!p->local_bound) return fail(PRAGHIP_E_STATE, "E_RESIDENT_LOCAL_SHAPE");
   if (int rc = token_check_ring(p, ring, words)) return rc;
   return token_finished_host(p, ring, words, nullptr, view);
+}
+
+int praghip_token_reserve(praghip_token_plan* p, size_t coords) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_RESIDENT_CLOSED");
+  if (coords == 0 || coords > 4096) return fail(PRAGHIP_E_SHAPE, "E_RESIDENT_BATCH");
+  if (coords <= p->batch_cap) return PRAGHIP_OK;
+  if (p->batch_cap) return fail(PRAGHIP_E_STATE, "E_RESIDENT_BATCH_RESERVED");
+  const size_t n = size_t(1) << p->log_n;
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->bweight, coords * p->blocks * p->P * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->boutput, coords * p->words * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->bscaled, coords * p->slots * p->P * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->bpartial, coords * p->slots * kLocalTiles * 8, true);
+  if (e != hipSuccess) return token_failure(p, e, "reserve");
+  p->batch_cap = coords;
+  p->timing.device_bytes = p->buf.total_bytes();
+  p->timing.sensitive_bytes = p->buf.sensitive_bytes();
+  return PRAGHIP_OK;
+}
+
+int praghip_token_evaluate_device_batch(praghip_token_plan* p, const uint64_t* rings, const uint64_t* residues,
+                                        uint64_t* output, size_t coords, void* stream) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_RESIDENT_CLOSED");
+  if (coords == 0) return PRAGHIP_OK;
+  if (!rings || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (coords > p->batch_cap) return fail(PRAGHIP_E_SHAPE, "E_RESIDENT_BATCH");
+  if (!residues && !p->local_bound) return fail(PRAGHIP_E_STATE, "E_RESIDENT_LOCAL_SHAPE");
+  if (!aligned8(rings) || !aligned8(output) || (residues && !aligned8(residues)))
+    return fail(PRAGHIP_E_ARGUMENT, "E_RESIDENT_ALIGNMENT");
+  const hipStream_t s = pick(stream);
+  const size_t limbs = p->slots * 2 * p->P, words = p->blocks * p->width;
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
+  const PrimeList pl = token_primes(p);
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_lift59(rings, p->bweight, coords * p->blocks, int(p->log_n), p->width, pl, s);
+  if (e == hipSuccess) e = launch_ntt(false, p->bweight, coords * p->blocks * p->P, p->d, s);
+  if (e == hipSuccess)
+    e = launch_token_mac(p->input, p->bweight, p->boutput, coords, p->blocks, limbs, int(p->log_n), m, int(p->P), s);
+  if (e == hipSuccess) e = launch_ntt(true, p->boutput, coords * limbs, p->d, s);
+  if (e == hipSuccess && !residues) {
+    e = launch_local_dot_scale(p->local_shares, rings, words, p->slots, p->delta.data(), p->r, m, int(p->P),
+                               p->bscaled, p->bpartial, s, coords);
+    residues = p->bscaled;
+  }
+  if (e == hipSuccess)
+    e = launch_token_finish(p->boutput, residues, output, coords * p->slots, pl, int(p->log_n), p->width, s);
+  if (e != hipSuccess) return token_failure(p, e, "evaluate_device_batch");
+  return PRAGHIP_OK;
 }
 
 int praghip_token_evaluate_device(praghip_token_plan* p, const uint64_t* ring, const uint64_t* residues,

@@ -80,6 +80,11 @@ struct PrimeList {
   uint64_t q[kMaxKeyPrimes];
   int count;
 };
+// Barrett-128 ratios of a prime list, passed by value.
+struct BarrettList {
+  Barrett m[kMaxKeyPrimes];
+  int count;
+};
 hipError_t launch_fill_residues(uint64_t* out, size_t words, int log_n, const PrimeList& q, uint64_t seed,
                                 hipStream_t s);
 hipError_t launch_fill_u64(uint64_t* out, size_t count, uint64_t seed, hipStream_t s);
@@ -100,14 +105,19 @@ hipError_t launch_dyadic_mac(const uint64_t* a, const uint64_t* w, uint64_t* out
                              int log_n, size_t w_limbs, const Barrett* m, int primes, hipStream_t s);
 hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,
                                   const uint64_t* delta, uint64_t r, const Barrett* m, int primes, uint64_t* scaled,
-                                  uint64_t* work, hipStream_t s);
+                                  uint64_t* work, hipStream_t s, size_t coords = 1);
 
 // Token-resident path and packing tree (token.hip).
 hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint64_t* out, size_t slots,
                                const PrimeList& pl, int log_n, size_t width, hipStream_t s);
+// out[c][l][N] = sum_b in[b][l] (.) w[c][b][l % P] over `coords` weight
+// columns sharing the resident inputs in [blocks][limbs][N]; w is
+// [coords][blocks][P][N], out [coords][limbs][N].
+hipError_t launch_token_mac(const uint64_t* in, const uint64_t* w, uint64_t* out, size_t coords, size_t blocks,
+                            size_t limbs, int log_n, const Barrett* m, int primes, hipStream_t s);
 hipError_t launch_pack_prepare(const uint64_t* left, const uint64_t* right, uint64_t* sum, uint64_t* diff,
                                size_t count, size_t first, size_t group, size_t stride, const PrimeList& pl,
-                               int log_n, size_t shift, uint32_t g, hipStream_t s);
+                               int log_n, size_t shift, uint32_t ginv, hipStream_t s);
 hipError_t launch_pack_finish(const uint64_t* a, const uint64_t* b, uint64_t* out, size_t count, const PrimeList& pl,
                               int log_n, hipStream_t s);
 

@@ -135,10 +135,6 @@ hipError_t launch_lift59(const uint64_t* ring, uint64_t* out, size_t blocks, int
 // out[l][z] = sum_b a[b][l][z] * w[b][l % wl][z] mod q_{l % P}: the Barrett-128
 // products of resident.cu:38-45 / matrix.cu:34-38, summed with a conditional
 // subtraction per block.  One thread per output word, the block loop inside.
-struct BarrettList {
-  Barrett m[kMaxKeyPrimes];
-  int count;
-};
 __global__ void dyadic_mac_kernel(const uint64_t* __restrict__ a, const uint64_t* __restrict__ w,
                                   uint64_t* __restrict__ out, size_t blocks, size_t limbs, int log_n, size_t w_limbs,
                                   BarrettList bl) {
@@ -193,16 +189,19 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* lds) {
   return s;
 }
 
+// Row y of the grid is (coordinate y / slots, slot y % slots): the slot's
+// shares against that coordinate's weights (coordinate c at weights + c words).
 __global__ void __launch_bounds__(256) local_dot_kernel(const uint64_t* __restrict__ shares,
                                                         const uint64_t* __restrict__ weights, size_t words,
-                                                        uint64_t* __restrict__ partial) {
+                                                        size_t slots, uint64_t* __restrict__ partial) {
   __shared__ uint64_t lds[4];
-  const size_t slot = blockIdx.y, g = blockIdx.x;
-  const uint64_t* s = shares + slot * words;
+  const size_t y = blockIdx.y, g = blockIdx.x;
+  const uint64_t* s = shares + (y % slots) * words;
+  const uint64_t* w = weights + (y / slots) * words;
   uint64_t acc = 0;
-  for (size_t j = g * blockDim.x + threadIdx.x; j < words; j += size_t(gridDim.x) * blockDim.x) acc += s[j] * weights[j];
+  for (size_t j = g * blockDim.x + threadIdx.x; j < words; j += size_t(gridDim.x) * blockDim.x) acc += s[j] * w[j];
   const uint64_t tot = block_sum_u64(acc, lds);
-  if (threadIdx.x == 0) partial[slot * gridDim.x + g] = tot;
+  if (threadIdx.x == 0) partial[y * gridDim.x + g] = tot;
 }
 
 __global__ void __launch_bounds__(256) local_scale_kernel(const uint64_t* __restrict__ partial, unsigned tiles,
@@ -223,9 +222,11 @@ __global__ void __launch_bounds__(256) local_scale_kernel(const uint64_t* __rest
   }
 }
 
+// coords > 1: `coords` weight columns of `words` each, one after the other;
+// scaled is [coords][slots][primes] and work [coords * slots][kLocalTiles].
 hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,
                                   const uint64_t* delta, uint64_t r, const Barrett* m, int primes, uint64_t* scaled,
-                                  uint64_t* work, hipStream_t s) {
+                                  uint64_t* work, hipStream_t s, size_t coords) {
   ScaleConst sc{};
   for (int i = 0; i < primes; ++i) {
     sc.m[i] = m[i];
@@ -234,10 +235,11 @@ hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weight
   sc.count = primes;
   sc.r = r;
   const unsigned tiles = unsigned(std::min<size_t>(kLocalTiles, std::max<size_t>(1, (words + 255) / 256)));
-  hipLaunchKernelGGL(local_dot_kernel, dim3(tiles, unsigned(slots)), dim3(256), 0, s, shares, weights, words, work);
+  const unsigned rows = unsigned(slots * coords);
+  hipLaunchKernelGGL(local_dot_kernel, dim3(tiles, rows), dim3(256), 0, s, shares, weights, words, slots, work);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(local_scale_kernel, dim3(unsigned(slots)), dim3(256), 0, s, work, tiles, sc, scaled);
+  hipLaunchKernelGGL(local_scale_kernel, dim3(rows), dim3(256), 0, s, work, tiles, sc, scaled);
   return hipGetLastError();
 }
 

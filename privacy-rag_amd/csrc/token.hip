@@ -9,7 +9,7 @@
 // All residues stay canonical (< q < 2^62, so a + b never wraps).  Each kernel
 // is a single HBM pass; one thread per output coefficient, contiguous in the
 // coefficient index so reads and writes coalesce except the Galois-permuted
-// write, which stays inside one 2^log_n-word limb.
+// reads, which stay inside one 2^log_n-word limb.
 #include "kernels.hpp"
 
 namespace praghip {
@@ -44,40 +44,116 @@ hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint6
   return hipGetLastError();
 }
 
+// Sum of products of a batch of weight columns against the resident inputs:
+//   out[c][l][z] = sum_b in[b][l][z] * w[c][b][l % P][z]  mod q_{l % P}
+// (resident.cu:38-45 accumulate, Barrett-128 as there), for every column c of
+// the batch.  One thread per (coordinate group, prime p, coefficient z) walks
+// all limbs l = p (mod P) and kMacCoords columns: each weight word is read once
+// and each input word once per column group, instead of once per column.
+constexpr int kMacCoords = 4, kMacLimbs = 8;
+__global__ void __launch_bounds__(256)
+    token_mac_kernel(const uint64_t* __restrict__ in, const uint64_t* __restrict__ w, uint64_t* __restrict__ out,
+                     size_t coords, size_t blocks, size_t limbs, int log_n, BarrettList bl) {
+  const size_t n = size_t(1) << log_n, P = size_t(bl.count), groups = (coords + kMacCoords - 1) / kMacCoords;
+  const size_t words = limbs << log_n, wcol = blocks * P << log_n, total = groups * P << log_n;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t z = i & (n - 1), p = (i >> log_n) % P, c0 = ((i >> log_n) / P) * kMacCoords;
+    const Barrett m = bl.m[p];
+    const size_t cn = coords - c0 < size_t(kMacCoords) ? coords - c0 : size_t(kMacCoords);
+    for (size_t l0 = p; l0 < limbs; l0 += kMacLimbs * P) {
+      uint64_t acc[kMacCoords][kMacLimbs];
+#pragma unroll
+      for (int c = 0; c < kMacCoords; ++c)
+#pragma unroll
+        for (int k = 0; k < kMacLimbs; ++k) acc[c][k] = 0;
+      for (size_t b = 0; b < blocks; ++b) {
+        uint64_t x[kMacLimbs];
+#pragma unroll
+        for (int k = 0; k < kMacLimbs; ++k) {
+          const size_t l = l0 + size_t(k) * P;
+          x[k] = l < limbs ? in[b * words + (l << log_n) + z] : 0;
+        }
+#pragma unroll
+        for (int c = 0; c < kMacCoords; ++c) {
+          if (size_t(c) >= cn) break;
+          const uint64_t wv = w[(c0 + c) * wcol + ((b * P + p) << log_n) + z];
+#pragma unroll
+          for (int k = 0; k < kMacLimbs; ++k) {
+            const uint64_t v = acc[c][k] + mul_barrett(x[k], wv, m);
+            acc[c][k] = v >= m.q ? v - m.q : v;
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < kMacCoords; ++c) {
+        if (size_t(c) >= cn) break;
+#pragma unroll
+        for (int k = 0; k < kMacLimbs; ++k) {
+          const size_t l = l0 + size_t(k) * P;
+          if (l < limbs) out[(c0 + c) * words + (l << log_n) + z] = acc[c][k];
+        }
+      }
+    }
+  }
+}
+
+hipError_t launch_token_mac(const uint64_t* in, const uint64_t* w, uint64_t* out, size_t coords, size_t blocks,
+                            size_t limbs, int log_n, const Barrett* m, int primes, hipStream_t s) {
+  BarrettList bl{};
+  for (int i = 0; i < primes; ++i) bl.m[i] = m[i];
+  bl.count = primes;
+  const size_t total = ((coords + kMacCoords - 1) / kMacCoords * size_t(primes)) << log_n;
+  hipLaunchKernelGGL(token_mac_kernel, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks, limbs,
+                     log_n, bl);
+  return hipGetLastError();
+}
+
 // Local pair i is pair e = first + i of the list; it reads
 // left(e) = left + ((e / group) * stride + e % group) * ct and right(e) the
 // same way from right (ct = 2 L N words), and writes
 //   sum[i]  = left(e) + x^shift right(e)
 //   diff[i] = sigma_g(left(e) - x^shift right(e)),  sigma_g: x -> x^g
-// with x^shift right at j = right[j - shift], negated for j < shift.
+// with x^shift right at j = right[j - shift], negated for j < shift.  Both
+// outputs are written in coefficient order: diff at d takes the source
+// coefficient u = d g^-1 mod 2N (negated when u >= N), gathered from inside
+// the same limb, so no write is scattered.
+__device__ __forceinline__ uint64_t shifted_diff(const uint64_t* __restrict__ l, const uint64_t* __restrict__ r,
+                                                 size_t j, size_t n, size_t shift, uint64_t q, uint64_t& sum) {
+  uint64_t v = r[(j + n - shift) & (n - 1)];
+  v = (j < shift && v) ? q - v : v;
+  const uint64_t a = l[j];
+  sum = add_mod(a, v, q);
+  return sub_mod(a, v, q);
+}
+
 __global__ void __launch_bounds__(256)
     pack_prepare_kernel(const uint64_t* __restrict__ left, const uint64_t* __restrict__ right,
                         uint64_t* __restrict__ sum, uint64_t* __restrict__ diff, size_t count, size_t first,
-                        size_t group, size_t stride, PrimeList pl, int log_n, size_t shift, uint32_t g) {
+                        size_t group, size_t stride, PrimeList pl, int log_n, size_t shift, uint32_t ginv) {
   const size_t n = size_t(1) << log_n, L = size_t(pl.count), ct = 2 * L * n, total = count * ct;
-  const size_t two_n_mask = 2 * n - 1;
   for (size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += size_t(gridDim.x) * blockDim.x) {
-    const size_t i = idx / ct, w = idx - i * ct, j = w & (n - 1), base = w - j, e = first + i;
+    const size_t i = idx / ct, w = idx - i * ct, d = w & (n - 1), base = w - d, e = first + i;
     const size_t src = ((e / group) * stride + e % group) * ct + base;
     const uint64_t q = pl.q[(w >> log_n) % L];
-    const bool neg = j < shift;
-    uint64_t v = right[src + ((j + n - shift) & (n - 1))];
-    v = (neg && v) ? q - v : v;
-    const uint64_t a = left[src + j];
-    sum[i * ct + w] = add_mod(a, v, q);
-    const uint64_t delta = sub_mod(a, v, q);
-    const size_t dest = (j * size_t(g)) & two_n_mask;
-    diff[i * ct + base + (dest & (n - 1))] = (dest >= n && delta) ? q - delta : delta;
+    const uint64_t* l = left + src;
+    const uint64_t* r = right + src;
+    uint64_t s0;
+    (void)shifted_diff(l, r, d, n, shift, q, s0);
+    sum[i * ct + w] = s0;
+    const size_t u = (d * size_t(ginv)) & (2 * n - 1);
+    uint64_t unused;
+    const uint64_t delta = shifted_diff(l, r, u & (n - 1), n, shift, q, unused);
+    diff[i * ct + w] = (u >= n && delta) ? q - delta : delta;
   }
 }
 
 hipError_t launch_pack_prepare(const uint64_t* left, const uint64_t* right, uint64_t* sum, uint64_t* diff,
                                size_t count, size_t first, size_t group, size_t stride, const PrimeList& pl,
-                               int log_n, size_t shift, uint32_t g, hipStream_t s) {
+                               int log_n, size_t shift, uint32_t ginv, hipStream_t s) {
   const size_t total = count * 2 * size_t(pl.count) << log_n;
   hipLaunchKernelGGL(pack_prepare_kernel, dim3(elem_grid(total)), dim3(256), 0, s, left, right, sum, diff, count,
-                     first, group, stride, pl, log_n, shift, g);
+                     first, group, stride, pl, log_n, shift, ginv);
   return hipGetLastError();
 }
 

@@ -90,6 +90,8 @@ SIGNATURES = {
     "praghip_token_evaluate_finished": (i32, [vp, vp, sz, vp, pp]),
     "praghip_token_evaluate_local_finished": (i32, [vp, vp, sz, pp]),
     "praghip_token_evaluate_device": (i32, [vp, vp, vp, vp, vp]),
+    "praghip_token_reserve": (i32, [vp, sz]),
+    "praghip_token_evaluate_device_batch": (i32, [vp, vp, vp, vp, sz, vp]),
     "praghip_token_stack_store": (i32, [vp, sz, ctypes.c_uint, vp, vp]),
     "praghip_token_stack_view": (i32, [vp, sz, ctypes.c_uint, pp]),
     "praghip_token_download": (i32, [vp, vp, vp]),

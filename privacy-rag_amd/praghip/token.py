@@ -87,6 +87,21 @@ class TokenWeights:
                                                   dev_ptr(out, u64_dtypes()), stream_handle(stream)))
         return out
 
+    def reserve(self, coords: int):
+        """Allocates the scratch of evaluate_device_batch for up to `coords` columns (once)."""
+        check(lib().praghip_token_reserve(self._h, coords))
+
+    def evaluate_device_batch(self, rings, out, residues=None, stream=None):
+        """rings: GPU [coords][blocks][width]; residues: GPU [coords][slots][P]
+        or None (bound shares); out: GPU [coords][slots][2][P][N]."""
+        coords = rings.numel() // (self.blocks * self.block_width)
+        if coords * self.blocks * self.block_width != rings.numel() or out.numel() != coords * self.slots * self.ct_words:
+            raise shape_error("E_RESIDENT_BATCH")
+        rp = None if residues is None else dev_ptr(residues, u64_dtypes())
+        check(lib().praghip_token_evaluate_device_batch(self._h, dev_ptr(rings, u64_dtypes()), rp,
+                                                        dev_ptr(out, u64_dtypes()), coords, stream_handle(stream)))
+        return out
+
     def slot_view(self, batch: DeviceCipherBatch, slot: int) -> DeviceCipherBatch:
         return DeviceCipherBatch(batch.data + slot * self.ct_words * 8, self.ct_words, batch.owner)
 

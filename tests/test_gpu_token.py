@@ -288,3 +288,46 @@ def test_token_loop_end_to_end(gpu):
     torch.cuda.synchronize()
     tw.close()
     pk.close()
+
+
+@pytest.mark.parametrize("log_n,P,blocks,slots,width,coords,locked", [(12, 3, 3, 2, 512, 6, False),
+                                                                       (14, 6, 19, 4, 8192, 5, True)])
+def test_token_batch(gpu, log_n, P, blocks, slots, width, coords, locked):
+    """evaluate_device_batch equals evaluate_device column by column (explicit
+    residues and bound shares), and the oracle on the first and last column."""
+    print(f"[token] batch log_n={log_n} coords={coords} slots={slots}", flush=True)
+    import torch
+    n = 1 << log_n
+    q = cf.LOCKED_PRIMES[:P] if locked else cf.primes_below(50, 2 * n, P)
+    ct = _inputs(q, n, blocks, slots, 900 + coords)
+    tw = praghip.TokenWeights(q, log_n, ct, width, levels=2)
+    tw.reserve(coords)
+    tw.reserve(coords - 1)          # a smaller request keeps the reservation
+    with pytest.raises(praghip.PraghipError, match="E_RESIDENT_BATCH_RESERVED"):
+        tw.reserve(coords + 1)
+    rings = np.stack([_ring(blocks, width, 910 + c, boundary=c == 1) for c in range(coords)])
+    locals_ = [[int(v) & MASK59 for v in oracle.fill_u64(slots, 930 + c)] for c in range(coords)]
+    res = np.stack([oracle.token_scaled(m, q) for m in locals_])
+    d_rings, d_res = to_dev(rings), to_dev(res)
+    out = torch.zeros(coords * slots * 2 * P * n, dtype=torch.int64, device="cuda")
+    tw.evaluate_device_batch(d_rings, out, residues=d_res)
+    one = torch.zeros(slots * 2 * P * n, dtype=torch.int64, device="cuda")
+    got = from_dev(out).reshape(coords, slots, 2, P, n)
+    for c in range(coords):
+        tw.evaluate_device(d_rings[c], one, residues=d_res[c])
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got[c], from_dev(one).reshape(slots, 2, P, n), err_msg=f"column {c}")
+    for c in (0, coords - 1):
+        np.testing.assert_array_equal(got[c], oracle.token_finished(ct, rings[c], res[c], q, log_n, width))
+    shares = (oracle.fill_u64(slots * blocks * width, 940) & np.uint64(MASK59)).reshape(slots, -1)
+    tw.bind_local_shares(shares)
+    tw.evaluate_device_batch(d_rings, out)
+    got = from_dev(out).reshape(coords, slots, 2, P, n)
+    for c in range(coords):
+        tw.evaluate_device(d_rings[c], one)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got[c], from_dev(one).reshape(slots, 2, P, n), err_msg=f"bound column {c}")
+    with pytest.raises(praghip.PraghipError, match="E_RESIDENT_BATCH"):
+        tw.evaluate_device_batch(to_dev(np.concatenate([rings, rings[:1]])),
+                                 torch.zeros((coords + 1) * slots * 2 * P * n, dtype=torch.int64, device="cuda"))
+    tw.close()
