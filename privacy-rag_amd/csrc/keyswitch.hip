@@ -278,18 +278,29 @@ __device__ __forceinline__ void ks_item_u64(const KsFused& f, const KsConst& kc,
     const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << LOGN);
     const uint64_t* k1 = k0 + (size_t(K) << LOGN);
 #pragma unroll
-    for (int r = 0; r < kE; ++r) {
-      const unsigned pos = fwd_out_index<LOGN>(th, r), si = unsigned(r) * TH + th;
-      const uint64_t x = ar.to_u64_fwd(e[r]);
-      uint64_t p0 = mul_barrett(x, k0[pos], bar);
-      uint64_t p1 = mul_barrett(x, k1[pos], bar);
-      if (j) {
-        p0 = add_mod(p0, s0[si], pr.q);
-        p1 = add_mod(p1, s1[si], pr.q);
+    for (int r = 0; r < kE; r += 2) {
+      // keys in 16-byte pairs (registers r, r + 1 are adjacent); the
+      // transformed digit meets two key words, so it gets a Shoup quotient
+      // and both products are Shoup products
+      const unsigned pos = fwd_out_index<LOGN>(th, r);
+      const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+      const ulonglong2 kb2 = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int rr = r + h;
+        const unsigned si = unsigned(rr) * TH + th;
+        const uint64_t x = ar.to_u64_fwd(e[rr]);
+        const uint64_t xq = shoup_quotient(x, bar);
+        uint64_t p0 = mul_shoup(h ? ka.y : ka.x, x, xq, pr.q);
+        uint64_t p1 = mul_shoup(h ? kb2.y : kb2.x, x, xq, pr.q);
+        if (j) {
+          p0 = add_mod(p0, s0[si], pr.q);
+          p1 = add_mod(p1, s1[si], pr.q);
+        }
+        s0[si] = p0;
+        s1[si] = p1;
       }
-      s0[si] = p0;
-      s1[si] = p1;
-      if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
     }
   }
   uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << LOGN);

@@ -70,6 +70,16 @@ PH_HD uint64_t mul_barrett(uint64_t a, uint64_t b, const Barrett m) {
   return rem >= m.q ? rem - m.q : rem;
 }
 
+// floor(w 2^64 / q) for w < q, from the Barrett ratio R = floor((2^128-1)/q):
+// t = w r1 + floor(w r0 / 2^64) = floor(w R / 2^64) fits 64 bits (w r1 < 2^64)
+// and is the quotient or one less, since R > 2^128/q - 1 and w < 2^64; the
+// remainder w 2^64 - t q lies in [0, 2q) and is exact mod 2^64.
+PH_HD uint64_t shoup_quotient(uint64_t w, const Barrett m) {
+  const uint64_t t = w * m.r1 + mulhi64(w, m.r0);
+  const uint64_t rem = 0 - t * m.q;
+  return rem >= m.q ? t + 1 : t;
+}
+
 // -------------------------------------------------------------------- float
 struct ShoupF {
   double w, wq;  // operand (exact integer), operand / q

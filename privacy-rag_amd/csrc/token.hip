@@ -46,10 +46,13 @@ hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint6
 
 // Sum of products of a batch of weight columns against the resident inputs:
 //   out[c][l][z] = sum_b in[b][l][z] * w[c][b][l % P][z]  mod q_{l % P}
-// (resident.cu:38-45 accumulate, Barrett-128 as there), for every column c of
-// the batch.  One thread per (coordinate group, prime p, coefficient z) walks
-// all limbs l = p (mod P) and kMacCoords columns: each weight word is read once
-// and each input word once per column group, instead of once per column.
+// (resident.cu:38-45 accumulate), for every column c of the batch.  One thread
+// per (coordinate group, prime p, coefficient z) walks all limbs l = p (mod P)
+// and kMacCoords columns: each weight word is read once and each input word
+// once per column group, instead of once per column.  A weight word meets up
+// to kMacLimbs inputs, so it gets a Shoup quotient (from the Barrett ratio)
+// and the products are Shoup products: exact, like the reference's Barrett-128
+// products, with fewer 64-bit multiplies.
 constexpr int kMacCoords = 4, kMacLimbs = 8;
 __global__ void __launch_bounds__(256)
     token_mac_kernel(const uint64_t* __restrict__ in, const uint64_t* __restrict__ w, uint64_t* __restrict__ out,
@@ -77,9 +80,10 @@ __global__ void __launch_bounds__(256)
         for (int c = 0; c < kMacCoords; ++c) {
           if (size_t(c) >= cn) break;
           const uint64_t wv = w[(c0 + c) * wcol + ((b * P + p) << log_n) + z];
+          const uint64_t wq = shoup_quotient(wv, m);
 #pragma unroll
           for (int k = 0; k < kMacLimbs; ++k) {
-            const uint64_t v = acc[c][k] + mul_barrett(x[k], wv, m);
+            const uint64_t v = acc[c][k] + mul_shoup(x[k], wv, wq, m.q);
             acc[c][k] = v >= m.q ? v - m.q : v;
           }
         }

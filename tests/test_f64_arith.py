@@ -51,3 +51,16 @@ def test_float_path_exact_and_bounded():
                     oracle.ntt(a[None], t)[0].tofile(f)
             r = subprocess.run([exe, path], capture_output=True, text=True)
             assert r.returncode == 0 and "ALL OK" in r.stdout, (q, lg, r.stdout, r.stderr)
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="no hipcc")
+def test_integer_helpers_exact():
+    """shoup_quotient, mul_shoup and mul_barrett of modarith.hpp against 128-bit host arithmetic."""
+    with tempfile.TemporaryDirectory() as d:
+        exe = os.path.join(d, "modarith_check")
+        subprocess.run([HIPCC, "-O2", "-std=c++17", "-x", "hip", "--offload-arch=gfx950",
+                        "-I", os.path.join(ROOT, "privacy-rag_amd", "csrc"),
+                        os.path.join(ROOT, "tests", "cpp", "modarith_check.cpp"), "-o", exe],
+                       check=True, capture_output=True)
+        r = subprocess.run([exe], capture_output=True, text=True)
+        assert r.returncode == 0 and "ALL OK" in r.stdout, r.stdout
