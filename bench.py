@@ -190,15 +190,18 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
     ct_words = 2 * P * N
     inputs = torch.empty(blocks * slots * ct_words, dtype=torch.int64, device="cuda")
     synth.fill_residues(inputs, q[:P], LOG_N, 0x5052414700000006)
-    tw = praghip.TokenWeights(q[:P], LOG_N, inputs.cpu().numpy().reshape(blocks, slots, 2, P, N), width, levels)
+    host_ct = inputs.cpu().numpy().reshape(blocks, slots, 2, P, N)
+    tw = praghip.TokenWeights(q[:P], LOG_N, host_ct, width, levels)
     del inputs
     shares = torch.empty(slots * blocks * width, dtype=torch.int64, device="cuda")
     synth.fill_u64(shares, 0x5052414700000106)
-    tw.bind_local_shares((shares & ((1 << 59) - 1)).cpu().numpy())
+    host_shares = (shares & ((1 << 59) - 1)).cpu().numpy()
+    tw.bind_local_shares(host_shares)
     del shares
     keys = torch.empty(levels * 2 * P * 2 * (P + 1) * N, dtype=torch.int64, device="cuda")
     synth.fill_residues(keys, q, LOG_N, 0x5052414700000206)
-    pk = praghip.Packing(q, LOG_N, keys.cpu().numpy(), dnum=P, max_pairs=512)
+    host_keys = keys.cpu().numpy()
+    pk = praghip.Packing(q, LOG_N, host_keys, dnum=P, max_pairs=512)
     del keys
     rings = torch.empty(coords * blocks * width, dtype=torch.int64, device="cuda")
     synth.fill_u64(rings, 0x5052414700000306)
@@ -219,12 +222,20 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
     ms = Timer(torch).run(step, steps, warmup)
     ms_eval = Timer(torch).run(evaluate_all, steps, 1)
     merges = (coords - 1) * slots
+    # samples for the CPU leg's parity: the finished batches of coordinates 0
+    # and 1, and their level-0 merge in slot 0
+    evaluate_all()
+    fin = nodes[:2].clone()
+    pair = pk.pair_device(fin[0, :ct_words], fin[1, :ct_words], 0)
+    torch.cuda.synchronize()
+    sample = {"q": q, "ct": host_ct, "shares": host_shares.reshape(slots, -1), "keys": host_keys,
+              "rings": rings[:2].cpu().numpy(), "finished": fin.cpu().numpy(), "pair": pair.cpu().numpy()}
     return {"slots": slots, "coordinates": coords, "blocks": blocks, "block_width": width, "levels": levels,
             "ms_per_step": ms, "ms_per_tile": ms, "coordinates_per_s": coords / (ms * 1e-3),
             "evaluate_ms_per_tile": ms_eval, "pack_ms_per_tile": ms - ms_eval,
             "merges_per_tile": merges, "pack_keyswitch_per_s": 2 * merges / ((ms - ms_eval) * 1e-3),
             "device_bytes": int(tw.timing().device_bytes + pk.timing().device_bytes),
-            "_plans": (tw, pk, rings, nodes)}
+            "_plans": (tw, pk, rings, nodes), "_sample": sample}
 
 
 def bench_copy(torch, steps, warmup):
@@ -287,6 +298,37 @@ def cpu_baselines(torch, res, budget_s: float):
     out["gemm_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
     out["gemm"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
                    "sample": f"{rows} of 512 activation rows x 1024 x 3072"}
+    # token tile: two coordinates' columns (resident inputs transformed once,
+    # as the GPU plan does at creation) and one level-0 merge, scaled to the
+    # tile's 512 columns and 2,044 merges
+    if "token" in res and "_sample" in res["token"]:
+        sm = res["token"]["_sample"]
+        qd, P, width = sm["q"][:6], 6, res["token"]["block_width"]
+        slots = sm["shares"].shape[0]
+        resident = oracle.token_inputs(sm["ct"], qd, LOG_N, threads)
+        Q = 1
+        for x in qd:
+            Q *= int(x)
+        delta, r = [(Q >> 59) % int(x) for x in qd], Q & ((1 << 59) - 1)
+        t0 = time.perf_counter()
+        fins = []
+        for c in range(2):
+            ring = sm["rings"][c].view(np.uint64)
+            scaled = oracle.local_dot_scale(sm["shares"], ring, delta, r, qd)
+            fins.append(oracle.token_finished(None, ring, scaled, qd, LOG_N, width, threads, resident=resident))
+        t_eval = (time.perf_counter() - t0) / 2
+        ok = all(np.array_equal(fins[c].reshape(-1), sm["finished"][c].view(np.uint64)) for c in range(2))
+        t0 = time.perf_counter()
+        pr = oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"], P, LOG_N,
+                              threads=threads)
+        t_pair = time.perf_counter() - t0
+        ok &= bool(np.array_equal(pr.reshape(-1), sm["pair"].view(np.uint64)))
+        coords, merges = res["token"]["coordinates"], res["token"]["merges_per_tile"]
+        tile_s = coords * t_eval + merges * t_pair
+        out["token_parity"] = ok
+        out["token"] = {"value": coords / tile_s, "unit": "coordinates/s", "cores": threads, "kind": "port",
+                        "sample": f"2 of 512 columns ({slots} slots, {t_eval * 1e3:.0f} ms each) and one level-0 "
+                                  f"merge ({t_pair * 1e3:.0f} ms), scaled to 512 columns + {merges} merges"}
     # Qwen3: the four products of layer 0 on 16 of the 512 token rows
     if "qwen3" in res and "_sample" in res["qwen3"]:
         ok, ops, dt = True, 0, 0.0
@@ -364,6 +406,8 @@ def main() -> int:
             f"evaluate {res['token']['evaluate_ms_per_tile']:.1f} ms)")
         res["token"]["steps"] = tsteps
         res["token"].pop("_plans")
+        if args.no_cpu or args.only != "all":
+            res["token"].pop("_sample")
     cpu = {}
     if not args.no_cpu and args.only == "all":
         log("oracle CPU baselines ...")

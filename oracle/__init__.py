@@ -321,6 +321,28 @@ def _monomial_shift_limbs(a: np.ndarray, q, log_n: int, e: int) -> np.ndarray:
     return out.reshape(np.shape(a))
 
 
+def token_inputs(ct: np.ndarray, q, log_n: int, threads: int = 0) -> np.ndarray:
+    """The resident form of TokenWeights' inputs (resident/seal_adapter.cpp:29-33):
+    ct [blocks][slots][2][P][N] coefficient form -> [blocks][slots*2*P][N] NTT form."""
+    n = 1 << log_n
+    ct = _u64(ct)
+    blocks = ct.shape[0]
+    return ntt(ct.reshape(-1, n), Tables(q, log_n), threads=threads).reshape(blocks, -1, n)
+
+
+def token_product(resident: np.ndarray, ring: np.ndarray, q, log_n: int, width: int, threads: int = 0) -> np.ndarray:
+    """sum_b resident_b (.) NTT(lift of ring_b reversed into coefficients
+    width-1..0) over NTT-form inputs [blocks][limbs][N] -> [limbs][N]
+    (resident.cu:143-145: lift, forward stages, accumulate)."""
+    n = 1 << log_n
+    P = len(q)
+    ring = _u64(ring)
+    blocks = ring.size // width
+    w = lift59_blocks(ring.reshape(blocks, width), q, n, width)            # [blocks][P][N]
+    wf = ntt(w.reshape(blocks * P, n), Tables(q, log_n), threads=threads).reshape(blocks, P, n)
+    return dyadic_mac(_u64(resident), wf, q)
+
+
 def token_evaluate(ct: np.ndarray, ring: np.ndarray, q, log_n: int, width: int, threads: int = 0) -> np.ndarray:
     """TokenWeights::evaluate (resident.cu:135-151; the CPU sequence of
     check_resident.cpp:51-59): ct [blocks][slots][2][P][N] coefficient form,
@@ -328,15 +350,8 @@ def token_evaluate(ct: np.ndarray, ring: np.ndarray, q, log_n: int, width: int, 
     sum_b NTT(ct_b) (.) NTT(lift of ring_b reversed into coefficients width-1..0)."""
     n = 1 << log_n
     P = len(q)
-    t = Tables(q, log_n)
-    ring = _u64(ring)
-    blocks = ring.size // width
-    ct = _u64(ct).reshape(blocks, -1, n)
-    slots = ct.shape[1] // (2 * P)
-    w = lift59_blocks(ring.reshape(blocks, width), q, n, width)            # [blocks][P][N]
-    wf = ntt(w.reshape(blocks * P, n), t, threads=threads).reshape(blocks, P, n)
-    cf_ = ntt(ct.reshape(-1, n), t, threads=threads).reshape(blocks, slots * 2 * P, n)
-    return dyadic_mac(cf_, wf, q).reshape(slots, 2, P, n)
+    acc = token_product(token_inputs(ct, q, log_n, threads), ring, q, log_n, width, threads)
+    return acc.reshape(-1, 2, P, n)
 
 
 def token_scaled(local, q, t_bits: int = 59) -> np.ndarray:
@@ -358,13 +373,16 @@ def token_scaled(local, q, t_bits: int = 59) -> np.ndarray:
 
 
 def token_finished(ct: np.ndarray, ring: np.ndarray, scaled: np.ndarray, q, log_n: int, width: int,
-                   threads: int = 0) -> np.ndarray:
+                   threads: int = 0, resident: np.ndarray | None = None) -> np.ndarray:
     """TokenWeights::evaluate_device (resident.cu:152-173): INTT of the
     evaluate() product, scaled[slot][k] added at coefficient width-1 of c0,
-    then the negacyclic shift by x^-(width-1) (add_shift, resident.cu:54-59)."""
+    then the negacyclic shift by x^-(width-1) (add_shift, resident.cu:54-59).
+    `resident` (token_inputs of ct) skips the inputs' transform."""
     n = 1 << log_n
     P = len(q)
-    acc = token_evaluate(ct, ring, q, log_n, width, threads)
+    if resident is None:
+        resident = token_inputs(ct, q, log_n, threads)
+    acc = token_product(resident, ring, q, log_n, width, threads).reshape(-1, 2, P, n)
     slots = acc.shape[0]
     coeff = ntt(acc.reshape(-1, n), Tables(q, log_n), inverse=True, threads=threads).reshape(slots, 2, P, n)
     qa = _u64(q)
