@@ -236,7 +236,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 // LDS: raw shares [2][32 rows][512 B], weights [2][128 rows][64 B] with the
 // 16-byte chunk index of row r stored at chunk ^ (r & 3) (conflict-free
 // operand reads without padding, which DMA cannot insert), digit planes
-// [8][32][80 B].
+// [8][34][80 B]: two spare rows per plane make the plane stride 2720 bytes
+// instead of 2560 (a multiple of the bank span), so the MFMA operand reads of
+// one row across the 8 digits spread over the banks (measured 3-5% faster).
 constexpr int kRawRow = kBK * 8;  // bytes of one raw share row per step
 
 // 16 bytes per lane from global memory straight into LDS at M0 + lane * 16
@@ -268,7 +270,7 @@ __device__ __forceinline__ void dma_issue(const DmaCtx& c, int k0, RAW& raw, WT&
 
 template <class RAW, class WT, class RAWN, class WTN>
 __device__ __forceinline__ void dma_step(const DmaCtx& c, bool next, int k_next, const RAW& raw, const WT& wt,
-                                         RAWN& raw_n, WTN& wt_n, uint8_t (&a_lds)[8][kBM][kPitch], int& colsum,
+                                         RAWN& raw_n, WTN& wt_n, uint8_t (&a_lds)[8][kBM + 2][kPitch], int& colsum,
                                          v16i (&acc)[4][2]) {
   // this wave's DMAs for this step are done (none other is in flight yet);
   // after the barrier every wave's are, and the previous step's reads are over
@@ -329,12 +331,12 @@ __device__ __forceinline__ void dma_step(const DmaCtx& c, bool next, int k_next,
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
     share_gemm_dma_kernel(const uint64_t* __restrict__ x, const int8_t* __restrict__ w,
                           const int8_t* __restrict__ shifts, uint64_t* __restrict__ y, int M, int K, int N,
-                          uint64_t mask) {
+                          uint64_t mask, int k_split) {
   __shared__ __attribute__((aligned(16))) uint8_t raw0[kBM * kRawRow];
   __shared__ __attribute__((aligned(16))) uint8_t raw1[kBM * kRawRow];
   __shared__ __attribute__((aligned(16))) uint8_t wt0[kBN * kBK];
   __shared__ __attribute__((aligned(16))) uint8_t wt1[kBN * kBK];
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM][kPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM + 2][kPitch];
   __shared__ int csum[kThreads];
 
   const int t = threadIdx.x, lane = t & 63;
@@ -373,12 +375,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16i{0};
 
-  dma_issue(c, 0, raw0, wt0);
-  const int steps = K / kBK;
+  // split-K: workgroup z takes K steps [z k_split, (z+1) k_split); with more
+  // than one split the partial products are added into y (zeroed first) by
+  // 64-bit atomics, exact mod 2^64 in any order
+  const int k_begin = int(blockIdx.z) * k_split;
+  const int steps = min(k_split, K - k_begin) / kBK;
+  dma_issue(c, k_begin, raw0, wt0);
   for (int s = 0; s < steps; s += 2) {
-    dma_step(c, s + 1 < steps, (s + 1) * kBK, raw0, wt0, raw1, wt1, a_lds, colsum, acc);
-    if (s + 1 < steps) dma_step(c, s + 2 < steps, (s + 2) * kBK, raw1, wt1, raw0, wt0, a_lds, colsum, acc);
+    dma_step(c, s + 1 < steps, k_begin + (s + 1) * kBK, raw0, wt0, raw1, wt1, a_lds, colsum, acc);
+    if (s + 1 < steps)
+      dma_step(c, s + 2 < steps, k_begin + (s + 2) * kBK, raw1, wt1, raw0, wt0, a_lds, colsum, acc);
   }
+  const bool split = gridDim.z > 1;
 
   // ---- epilogue: column sums, digit recombination, shift, mask
   csum[t] = colsum;
@@ -402,10 +410,19 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int dg = 0; dg < 8; ++dg) v += uint64_t(int64_t(acc[rb][cb][8 * a + dg])) << (8 * dg);
         v = sh < 64 ? (v << sh) : 0;
-        y[size_t(row) * N + col] = v & mask;
+        if (split)
+          atomicAdd(reinterpret_cast<unsigned long long*>(y + size_t(row) * N + col), (unsigned long long)v);
+        else
+          y[size_t(row) * N + col] = v & mask;
       }
     }
   }
+}
+
+// y = 0 before a split-K product (keep = 0); y &= mask after one (mask_bits < 64).
+__global__ void __launch_bounds__(256) gemm_fill_kernel(uint64_t* __restrict__ y, size_t n, uint64_t keep) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    y[i] = keep ? (y[i] & keep) : 0;
 }
 
 hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
@@ -416,9 +433,30 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
   const int w_vec = (K % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
   if (w_bits == 8) {
     if (K % kBK == 0 && w_vec && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-      hipLaunchKernelGGL(share_gemm_dma_kernel, grid, block, 0, s, x, static_cast<const int8_t*>(w), shifts, y, M,
-                         K, N, mask);
-      return hipGetLastError();
+      // Split K while the tiles fill fewer than 256 workgroups (one per CU;
+      // N = 1024 at M = 512 gives 128 tiles) and each split keeps >= 8 steps:
+      // measured 37 -> 26 us at 512x2048x1024 and 54 -> 33 us at 512x3072x1024,
+      // while going on to two workgroups per CU was slower.
+      const int tiles = int(grid.x * grid.y), ksteps = K / kBK;
+      int splits = 1;
+      while (splits < 4 && tiles * splits < 256 && ksteps / (splits * 2) >= 8) splits *= 2;
+      const int k_split = (ksteps + splits - 1) / splits * kBK;
+      splits = (K + k_split - 1) / k_split;
+      const size_t words = size_t(M) * N;
+      const unsigned fgrid = unsigned(std::min<size_t>((words + 255) / 256, 4096));
+      if (splits > 1) {
+        hipLaunchKernelGGL(gemm_fill_kernel, dim3(fgrid), dim3(256), 0, s, y, words, 0ull);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(share_gemm_dma_kernel, dim3(grid.x, grid.y, unsigned(splits)), block, 0, s, x,
+                         static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split);
+      hipError_t e = hipGetLastError();
+      if (e == hipSuccess && splits > 1 && mask != ~0ull) {
+        hipLaunchKernelGGL(gemm_fill_kernel, dim3(fgrid), dim3(256), 0, s, y, words, mask);
+        e = hipGetLastError();
+      }
+      return e;
     }
     hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, 0, 0, w_vec);
     return hipGetLastError();

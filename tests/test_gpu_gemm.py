@@ -73,3 +73,16 @@ def test_gemm_c4_full_shape(gpu):
     x = oracle.fill_u64(m * k, 0x5052414700000004).reshape(m, k)
     w = oracle.fill_i8(n * k, 0x5052414700000104).reshape(n, k)
     np.testing.assert_array_equal(_run(x, w), oracle.share_gemm(x, w))
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 2048, 1024), (512, 3072, 1024), (96, 4096, 256)])
+def test_gemm_split_k_shapes(gpu, m, k, n):
+    """Shapes whose tiles leave most workgroup slots empty run split-K (64-bit
+    atomic accumulation into a zeroed y, then the 59-bit mask): the Qwen3 o
+    and down products, and a long-K thin case."""
+    print(f"[gemm] split-K m={m} k={k} n={n}", flush=True)
+    x = oracle.fill_u64(m * k, 5000 + k).reshape(m, k)
+    w = oracle.fill_i8(n * k, 6000 + k).reshape(n, k)
+    sh = oracle.fill_shift(n, 7000 + k)
+    for shifts, mask in ((None, 64), (sh, 59)):
+        np.testing.assert_array_equal(_run(x, w, shifts, mask), oracle.share_gemm(x, w, shifts, mask))
