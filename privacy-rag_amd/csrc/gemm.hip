@@ -420,7 +420,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 }
 
 // y = 0 before a split-K product (keep = 0); y &= mask after one (mask_bits < 64).
-__global__ void __launch_bounds__(256) gemm_fill_kernel(uint64_t* __restrict__ y, size_t n, uint64_t keep) {
+__global__ void __launch_bounds__(256) gemm_clear_kernel(uint64_t* __restrict__ y, size_t n, uint64_t keep) {
   for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
     y[i] = keep ? (y[i] & keep) : 0;
 }
@@ -445,7 +445,7 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
       const size_t words = size_t(M) * N;
       const unsigned fgrid = unsigned(std::min<size_t>((words + 255) / 256, 4096));
       if (splits > 1) {
-        hipLaunchKernelGGL(gemm_fill_kernel, dim3(fgrid), dim3(256), 0, s, y, words, 0ull);
+        hipLaunchKernelGGL(gemm_clear_kernel, dim3(fgrid), dim3(256), 0, s, y, words, 0ull);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
       }
@@ -453,7 +453,7 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
                          static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split);
       hipError_t e = hipGetLastError();
       if (e == hipSuccess && splits > 1 && mask != ~0ull) {
-        hipLaunchKernelGGL(gemm_fill_kernel, dim3(fgrid), dim3(256), 0, s, y, words, mask);
+        hipLaunchKernelGGL(gemm_clear_kernel, dim3(fgrid), dim3(256), 0, s, y, words, mask);
         e = hipGetLastError();
       }
       return e;
