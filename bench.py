@@ -358,7 +358,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+        print(f"bench.py measures one GPU: praghip has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
     import torch

@@ -1,7 +1,7 @@
 """CPU oracle for the BFV NTT / keyswitch / share-GEMM path (ctypes over liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` and
-by the cpu_baseline leg of ``bench.py``, and there only as the checker.  The
+by the cpu_baseline leg of ``bench.py``, and there only to check results.  The
 product package never imports it.
 
 The C restatement lives in ``oracle.c`` (each function cites the reference

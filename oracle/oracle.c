@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the BFV polynomial engine and the party-local share GEMM.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker: it is linked or called
+ * TEST INFRASTRUCTURE ONLY.  It checks results: it is linked or called
  * only by tests/, by __graft_entry__.smoke() and by the cpu_baseline leg of
  * bench.py.  The product library (privacy-rag_amd/) never calls it and never
  * falls back to it.

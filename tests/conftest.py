@@ -20,7 +20,7 @@ def golden_dir():
 
 @pytest.fixture(scope="session")
 def gpu():
-    """torch device handle for the -m gpu tests (they only run on the GPU box)."""
+    """torch device handle for the -m gpu tests (they need a gfx950 GPU)."""
     import torch
     if not torch.cuda.is_available():
         pytest.skip("no GPU in this environment")
