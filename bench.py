@@ -238,6 +238,61 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
             "_plans": (tw, pk, rings, nodes), "_sample": sample}
 
 
+def bench_matrix(torch, praghip, steps, warmup, blocks=3, groups=64):
+    """The HE matrix product at the reference shape (matrix.cu:48-81: N=16384,
+    six 60-bit primes): `blocks` resident ciphertext blocks, one evaluation
+    per output group (weight ring [blocks][N]), 64 groups back to back."""
+    from praghip import params, synth
+    q = list(params.LOCKED_PRIMES[:6])
+    P = 6
+    ct = torch.empty(blocks * 2 * P * N, dtype=torch.int64, device="cuda")
+    synth.fill_residues(ct, q, LOG_N, 0x5052414700000007)
+    host_ct = ct.cpu().numpy().reshape(blocks, 2, P, N)
+    m = praghip.Matrix(q, LOG_N, host_ct)
+    rings = torch.empty(groups * blocks * N, dtype=torch.int64, device="cuda")
+    synth.fill_u64(rings, 0x5052414700000107)
+    rings = (rings & ((1 << 59) - 1)).view(groups, blocks * N)
+    out = torch.empty((groups, 2 * P * N), dtype=torch.int64, device="cuda")
+
+    def step():
+        for g in range(groups):
+            m.evaluate_device(rings[g], out[g])
+
+    ms = Timer(torch).run(step, steps, warmup)
+    torch.cuda.synchronize()
+    return {"blocks": blocks, "groups_per_step": groups, "ms_per_step": ms,
+            "evaluations_per_s": groups / (ms * 1e-3), "us_per_evaluation": ms * 1e3 / groups,
+            "_sample": {"q": q, "ct": host_ct, "ring": rings[0].cpu().numpy(), "out": out[0].cpu().numpy()},
+            "_keep": (m,)}
+
+
+def bench_enc0(torch, praghip, steps, warmup, count=64):
+    """Public-key encryption of zero at the reference shape (enc0.cu:99-114:
+    N=16384, six 60-bit data primes + the special prime): `count`
+    encryptions back to back, each from its own samples [3][7][N]."""
+    from praghip import params, synth
+    q = list(params.LOCKED_PRIMES)
+    K = 7
+    pk = torch.empty(2 * K * N, dtype=torch.int64, device="cuda")
+    synth.fill_residues(pk, q, LOG_N, 0x5052414700000008)
+    host_pk = pk.cpu().numpy().reshape(2, K, N)
+    z = praghip.PublicZero(q, LOG_N, host_pk)
+    samples = torch.empty((count, 3 * K * N), dtype=torch.int64, device="cuda")
+    synth.fill_residues(samples, q, LOG_N, 0x5052414700000108)
+    out = torch.empty((count, 2 * (K - 1) * N), dtype=torch.int64, device="cuda")
+
+    def step():
+        for i in range(count):
+            z.evaluate_device(samples[i], out[i])
+
+    ms = Timer(torch).run(step, steps, warmup)
+    torch.cuda.synchronize()
+    return {"encryptions_per_step": count, "ms_per_step": ms, "encryptions_per_s": count / (ms * 1e-3),
+            "us_per_encryption": ms * 1e3 / count,
+            "_sample": {"q": q, "pk": host_pk, "samples": samples[0].cpu().numpy(), "out": out[0].cpu().numpy()},
+            "_keep": (z,)}
+
+
 def bench_copy(torch, steps, warmup):
     """Plain device copy of 384 MiB (the bytes one NTT launch reads, and again writes):
     the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -329,6 +384,24 @@ def cpu_baselines(torch, res, budget_s: float):
         out["token"] = {"value": coords / tile_s, "unit": "coordinates/s", "cores": threads, "kind": "port",
                         "sample": f"2 of 512 columns ({slots} slots, {t_eval * 1e3:.0f} ms each) and one level-0 "
                                   f"merge ({t_pair * 1e3:.0f} ms), scaled to 512 columns + {merges} merges"}
+    # HE matrix product and encryption of zero: one evaluation each, with parity
+    if "matrix" in res and "_sample" in res["matrix"]:
+        sm = res["matrix"]["_sample"]
+        t0 = time.perf_counter()
+        want = oracle.matrix_product(sm["ct"], sm["ring"].view(np.uint64), sm["q"], LOG_N, threads=threads)
+        dt = time.perf_counter() - t0
+        out["matrix_parity"] = bool(np.array_equal(want.reshape(-1), sm["out"].view(np.uint64)))
+        out["matrix"] = {"value": 1 / dt, "unit": "evaluations/s", "cores": threads, "kind": "port",
+                         "sample": f"one evaluation ({res['matrix']['blocks']} blocks, N=16384, 6 primes), "
+                                   "inputs transformed inside the sample"}
+    if "enc0" in res and "_sample" in res["enc0"]:
+        sm = res["enc0"]["_sample"]
+        t0 = time.perf_counter()
+        want = oracle.enc0(sm["samples"].view(np.uint64).reshape(3, 7, N), sm["pk"].view(np.uint64), sm["q"], LOG_N)
+        dt = time.perf_counter() - t0
+        out["enc0_parity"] = bool(np.array_equal(want.reshape(-1), sm["out"].view(np.uint64)))
+        out["enc0"] = {"value": 1 / dt, "unit": "encryptions/s", "cores": 1, "kind": "port",
+                       "sample": "one encryption of zero (N=16384, 6 + 1 primes)"}
     # Qwen3: the four products of layer 0 on 16 of the 512 token rows
     if "qwen3" in res and "_sample" in res["qwen3"]:
         ok, ops, dt = True, 0, 0.0
@@ -352,7 +425,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "qwen3", "token", "copy"],
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "gemm", "qwen3", "token", "matrix", "enc0", "copy"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
@@ -408,6 +481,14 @@ def main() -> int:
         res["token"].pop("_plans")
         if args.no_cpu or args.only != "all":
             res["token"].pop("_sample")
+    for name, fn, unit in (("matrix", bench_matrix, "evaluations_per_s"), ("enc0", bench_enc0, "encryptions_per_s")):
+        if args.only in ("all", name):
+            log(f"{name} ...")
+            res[name] = fn(torch, praghip, max(1, min(args.steps, 10)), 2)
+            res[name].pop("_keep")
+            log(f"{name} {res[name][unit]:.4g}/s")
+            if args.no_cpu or args.only != "all":
+                res[name].pop("_sample")
     cpu = {}
     if not args.no_cpu and args.only == "all":
         log("oracle CPU baselines ...")
@@ -417,13 +498,14 @@ def main() -> int:
     def clean(d):
         return {k: v for k, v in d.items() if not k.startswith("_")}
 
-    key = next(k for k in ("ntt", "keyswitch", "gemm", "qwen3", "token") if k in res)
+    key = next(k for k in ("ntt", "keyswitch", "gemm", "qwen3", "token", "matrix", "enc0") if k in res)
     primary = res[key]
     value = {"ntt": lambda r: r["ntt_per_s"], "keyswitch": lambda r: r["keyswitch_per_s"],
              "gemm": lambda r: r["tops"], "qwen3": lambda r: r["tops"],
-             "token": lambda r: r["coordinates_per_s"]}[key](primary)
+             "token": lambda r: r["coordinates_per_s"], "matrix": lambda r: r["evaluations_per_s"],
+             "enc0": lambda r: r["encryptions_per_s"]}[key](primary)
     unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "gemm": "TOPS", "qwen3": "TOPS",
-            "token": "coordinates/s"}[key]
+            "token": "coordinates/s", "matrix": "evaluations/s", "enc0": "encryptions/s"}[key]
     line = {
         "metric": METRIC,
         "value": value,
@@ -443,7 +525,9 @@ def main() -> int:
             "keyswitch": "keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
             "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64",
             "qwen3": "Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens",
-            "token": "token-resident tile, 512 coordinates x 4 slots, 19 blocks of 8192, 9-level packing"}[key],
+            "token": "token-resident tile, 512 coordinates x 4 slots, 19 blocks of 8192, 9-level packing",
+            "matrix": "HE matrix product, N=16384, 6 primes, 3 blocks, 64 output groups",
+            "enc0": "public-key encryption of zero, N=16384, 6 + 1 primes, 64 encryptions"}[key],
             "N": N, "parallelism": "single GPU"},
         "roofline": primary.get("roofline"),
         "cpu_baseline": cpu.get(key),
