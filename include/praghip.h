@@ -208,15 +208,25 @@ int praghip_local_dot_scale(int device, const uint64_t *shares, const uint64_t *
  * is written to host [2][primes][2^log_n].  With `targets` (1..512 strictly
  * increasing coefficient indices, evaluate_selective) the c0 coefficients
  * outside the targets are zero.  evaluate_device: the same on device buffers,
- * asynchronous on `stream`, full output.  Errors MATRIX_GPU_SHAPE,
- * MATRIX_GPU_TARGET_COUNT, MATRIX_GPU_TARGET_INDEX, E_NTT_CANONICAL_REQUIRED;
- * a device error poisons the plan. */
+ * asynchronous on `stream`, full output.  reserve + evaluate_device_batch:
+ * `groups` independent evaluations in one call (the loop the reference runs as
+ * one Matrix::evaluate per output group, bfv_matrix.inc:101-105), rings
+ * [groups][blocks][2^log_n] and out [groups][2][primes][2^log_n], both
+ * 16-byte aligned device buffers; reserve(groups) allocates the batch scratch
+ * once (MATRIX_GPU_BATCH above the reserved count or 4096,
+ * MATRIX_GPU_BATCH_RESERVED on a larger second reserve).  Errors
+ * MATRIX_GPU_SHAPE, MATRIX_GPU_TARGET_COUNT, MATRIX_GPU_TARGET_INDEX,
+ * MATRIX_GPU_ALIGNMENT, E_NTT_CANONICAL_REQUIRED; a device error poisons the
+ * plan. */
 typedef struct praghip_matrix_plan praghip_matrix_plan;
 int praghip_matrix_plan_create(int device, const uint64_t *q, size_t primes, uint32_t log_n, const uint64_t *input,
                                size_t blocks, praghip_matrix_plan **plan);
 int praghip_matrix_evaluate(praghip_matrix_plan *plan, const uint64_t *ring, uint64_t *output,
                             const uint64_t *targets, size_t count);
 int praghip_matrix_evaluate_device(praghip_matrix_plan *plan, const uint64_t *ring, uint64_t *output, void *stream);
+int praghip_matrix_reserve(praghip_matrix_plan *plan, size_t groups);
+int praghip_matrix_evaluate_device_batch(praghip_matrix_plan *plan, const uint64_t *rings, uint64_t *output,
+                                         size_t groups, void *stream);
 size_t praghip_matrix_device_bytes(const praghip_matrix_plan *plan);
 int praghip_matrix_close(praghip_matrix_plan *plan, praghip_cleanup *out);
 void praghip_matrix_destroy(praghip_matrix_plan *plan);
@@ -229,13 +239,21 @@ void praghip_matrix_destroy(praghip_matrix_plan *plan);
  * writes out[c] = ModDown(INTT(NTT(u) (.) pk_c) + e_c), host [2][L][N], then
  * wipes every device intermediate.  evaluate_device: the same on device
  * buffers (samples [3][K][N], out [2][L][N]), asynchronous on `stream`.
- * Errors as Switch (E_SWITCH_SHAPE, E_SWITCH_CLOSED); a device error poisons
- * the plan. */
+ * reserve + evaluate_device_batch: `count` encryptions in one call (the
+ * per-ciphertext loop of enc0.cu:99-114 callers), samples [count][3][K][N]
+ * and out [count][2][L][N], 16-byte aligned device buffers; reserve(count)
+ * allocates the batch scratch once (E_ENC0_BATCH above the reserved count or
+ * 4096, E_ENC0_BATCH_RESERVED on a larger second reserve).  Errors as Switch
+ * (E_SWITCH_SHAPE, E_SWITCH_CLOSED) and E_ENC0_ALIGNMENT; a device error
+ * poisons the plan. */
 typedef struct praghip_enc0_plan praghip_enc0_plan;
 int praghip_enc0_plan_create(int device, const uint64_t *q, size_t data_primes, uint32_t log_n, const uint64_t *pk,
                              praghip_enc0_plan **plan);
 int praghip_enc0_evaluate(praghip_enc0_plan *plan, const uint64_t *samples, uint64_t *output);
 int praghip_enc0_evaluate_device(praghip_enc0_plan *plan, const uint64_t *samples, uint64_t *output, void *stream);
+int praghip_enc0_reserve(praghip_enc0_plan *plan, size_t count);
+int praghip_enc0_evaluate_device_batch(praghip_enc0_plan *plan, const uint64_t *samples, uint64_t *output,
+                                       size_t count, void *stream);
 int praghip_enc0_close(praghip_enc0_plan *plan, praghip_cleanup *out);
 void praghip_enc0_destroy(praghip_enc0_plan *plan);
 

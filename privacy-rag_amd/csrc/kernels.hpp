@@ -71,9 +71,10 @@ struct Enc0Const {
   uint64_t half_mod[kMaxKeyPrimes];  // floor(p/2) mod q_i
   uint64_t one_q[kMaxKeyPrimes];     // floor(2^64 / q_i)
 };
-// out [2][L][N] = ModDown(prod + noise), prod and noise [2][K][N].
+// out [2][L][N] = ModDown(prod + noise), prod and noise [2][K][N]; for `count`
+// encryptions prod and out advance by their size and noise by noise_stride.
 hipError_t launch_enc0_moddown(const uint64_t* prod, const uint64_t* noise, uint64_t* out, const Enc0Const& kc,
-                               hipStream_t s);
+                               hipStream_t s, size_t count = 1, size_t noise_stride = 0);
 
 // Prime list passed by value to the fill kernel.
 struct PrimeList {

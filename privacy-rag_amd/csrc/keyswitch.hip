@@ -61,18 +61,22 @@ __global__ void __launch_bounds__(256)
 // switch.cu:74-82 without the c0 term.
 __global__ void __launch_bounds__(256)
     enc0_moddown_kernel(const uint64_t* __restrict__ prod, const uint64_t* __restrict__ noise,
-                        uint64_t* __restrict__ out, Enc0Const kc) {
+                        uint64_t* __restrict__ out, Enc0Const kc, size_t count, size_t noise_stride) {
   const int L = kc.L, K = L + 1, log_n = kc.log_n;
-  const size_t n = size_t(1) << log_n, total = size_t(2 * L) << log_n;
+  const size_t n = size_t(1) << log_n, per = size_t(2 * L) << log_n, total = count * per;
   const uint64_t p = kc.q[L], half = p >> 1;
   for (size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += size_t(gridDim.x) * blockDim.x) {
-    const size_t c = idx / (size_t(L) << log_n), k = idx & (n - 1);
-    const int i = int((idx >> log_n) % unsigned(L));
+    // encryption e: prod + e [2][K][N], noise + e noise_stride, out + e [2][L][N]
+    const size_t e = idx / per, r = idx - e * per;
+    const size_t c = r / (size_t(L) << log_n), k = r & (n - 1);
+    const int i = int((r >> log_n) % unsigned(L));
     const uint64_t qi = kc.q[i];
+    const uint64_t* pe = prod + e * (size_t(2 * K) << log_n);
+    const uint64_t* ne = noise + e * noise_stride;
     const size_t li = (c * K + i) * n + k, lp = (c * K + L) * n + k;
-    const uint64_t x = add_mod(prod[li], noise[li], qi);
-    uint64_t last = add_mod(prod[lp], noise[lp], p) + half;
+    const uint64_t x = add_mod(pe[li], ne[li], qi);
+    uint64_t last = add_mod(pe[lp], ne[lp], p) + half;
     last = last >= p ? last - p : last;
     const uint64_t reduced = mul_shoup(last, 1, kc.one_q[i], qi);  // last mod q_i
     const uint64_t corr = sub_mod(reduced, kc.half_mod[i], qi);
@@ -81,10 +85,10 @@ __global__ void __launch_bounds__(256)
 }
 
 hipError_t launch_enc0_moddown(const uint64_t* prod, const uint64_t* noise, uint64_t* out, const Enc0Const& kc,
-                               hipStream_t s) {
-  const size_t total = size_t(2 * kc.L) << kc.log_n;
+                               hipStream_t s, size_t count, size_t noise_stride) {
+  const size_t total = count * (size_t(2 * kc.L) << kc.log_n);
   const unsigned blocks = unsigned(std::min<size_t>((total + 255) / 256, 1u << 16));
-  hipLaunchKernelGGL(enc0_moddown_kernel, dim3(blocks), dim3(256), 0, s, prod, noise, out, kc);
+  hipLaunchKernelGGL(enc0_moddown_kernel, dim3(blocks), dim3(256), 0, s, prod, noise, out, kc, count, noise_stride);
   return hipGetLastError();
 }
 
@@ -99,8 +103,9 @@ hipError_t launch_enc0_moddown(const uint64_t* prod, const uint64_t* noise, uint
 //
 // Arithmetic per prime: the float path when every data prime and t are below
 // 2^50 (ModUp, product and transforms in exact FP64), otherwise the integer
-// path (Shoup ModUp, Barrett-128 products as in switch.cu:30-45, Harvey
-// transforms).  The special prime (60 bits) takes the integer path.
+// path (Shoup ModUp, Shoup key products exact like the Barrett-128 products of
+// switch.cu:30-45, Harvey transforms).  The special prime (60 bits) takes the
+// integer path.
 struct KsFused {
   const uint64_t* in;      // [batch][2][L][N]
   const uint64_t* key;     // [dnum][2][K][N] per key, key_stride words apart

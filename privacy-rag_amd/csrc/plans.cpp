@@ -27,6 +27,8 @@ struct praghip_matrix_plan {
   Buffers buf;
   NttDevice d;
   uint64_t *input = nullptr, *ring = nullptr, *weight = nullptr, *output = nullptr;
+  size_t batch_cap = 0;
+  uint64_t* bweight = nullptr;  // [batch_cap][blocks][P][N] transformed weight limbs
   hipStream_t stream = nullptr;
   hipEvent_t ev[1] = {};
   praghip_cleanup cleanup{};
@@ -138,6 +140,49 @@ int praghip_matrix_evaluate_device(praghip_matrix_plan* p, const uint64_t* ring,
   return PRAGHIP_OK;
 }
 
+int praghip_matrix_reserve(praghip_matrix_plan* p, size_t groups) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "MATRIX_GPU_CLOSED");
+  if (groups == 0 || groups > 4096) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_BATCH");
+  if (groups <= p->batch_cap) return PRAGHIP_OK;
+  if (p->batch_cap) return fail(PRAGHIP_E_STATE, "MATRIX_GPU_BATCH_RESERVED");
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->bweight, groups * p->blocks * p->P * (size_t(8) << p->log_n), true);
+  if (e != hipSuccess) return matrix_failure(p, e, "reserve");
+  p->batch_cap = groups;
+  return PRAGHIP_OK;
+}
+
+// Many output groups per call: lift and transform every group's weight limbs,
+// one column-batched sum of products over the resident blocks, one inverse
+// transform over all outputs.
+int praghip_matrix_evaluate_device_batch(praghip_matrix_plan* p, const uint64_t* rings, uint64_t* output,
+                                         size_t groups, void* stream) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "MATRIX_GPU_CLOSED");
+  if (groups == 0) return PRAGHIP_OK;
+  if (!rings || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (groups > p->batch_cap) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_BATCH");
+  if ((reinterpret_cast<uintptr_t>(rings) | reinterpret_cast<uintptr_t>(output)) & 15)
+    return fail(PRAGHIP_E_ARGUMENT, "MATRIX_GPU_ALIGNMENT");
+  PrimeList pl{};
+  for (size_t i = 0; i < p->P; ++i) pl.q[i] = p->host_q[i];
+  pl.count = int(p->P);
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
+  const hipStream_t s = pick(stream);
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_lift59(rings, p->bweight, groups * p->blocks, int(p->log_n), 0, pl, s);
+  if (e == hipSuccess) e = launch_ntt(false, p->bweight, groups * p->blocks * p->P, p->d, s);
+  if (e == hipSuccess)
+    e = launch_token_mac(p->input, p->bweight, output, groups, p->blocks, 2 * p->P, int(p->log_n), m, int(p->P), s);
+  if (e == hipSuccess) e = launch_ntt(true, output, groups * 2 * p->P, p->d, s);
+  if (e != hipSuccess) return matrix_failure(p, e, "evaluate_device_batch");
+  return PRAGHIP_OK;
+}
+
 size_t praghip_matrix_device_bytes(const praghip_matrix_plan* p) { return p ? p->buf.total_bytes() : 0; }
 
 int praghip_matrix_close(praghip_matrix_plan* p, praghip_cleanup* out) {
@@ -163,6 +208,8 @@ struct praghip_enc0_plan {
   NttDevice d;
   Enc0Const kc{};
   uint64_t *pk = nullptr, *samples = nullptr, *expanded = nullptr, *prod = nullptr, *out = nullptr;
+  size_t batch_cap = 0;
+  uint64_t *bu = nullptr, *bprod = nullptr;  // [batch_cap][K][N] NTT(u), [batch_cap][2][K][N] products
   hipStream_t stream = nullptr;
   hipEvent_t ev[1] = {};
   praghip_cleanup cleanup{};
@@ -272,6 +319,52 @@ int praghip_enc0_evaluate_device(praghip_enc0_plan* p, const uint64_t* samples, 
   hipError_t e = scope.status();
   if (e == hipSuccess) e = enc0_run(p, samples, output, pick(stream));
   if (e != hipSuccess) return enc0_failure(p, e, "evaluate");
+  return PRAGHIP_OK;
+}
+
+int praghip_enc0_reserve(praghip_enc0_plan* p, size_t count) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  if (count == 0 || count > 4096) return fail(PRAGHIP_E_SHAPE, "E_ENC0_BATCH");
+  if (count <= p->batch_cap) return PRAGHIP_OK;
+  if (p->batch_cap) return fail(PRAGHIP_E_STATE, "E_ENC0_BATCH_RESERVED");
+  const size_t limb = size_t(8) << p->log_n;
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->bu, count * p->K * limb, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->bprod, count * 2 * p->K * limb, true);
+  if (e != hipSuccess) return enc0_failure(p, e, "reserve");
+  p->batch_cap = count;
+  return PRAGHIP_OK;
+}
+
+// Many encryptions per call: every u transformed in one launch, the products
+// with both key components as one column-batched product (the public key is
+// the single resident block), one inverse transform, one noise-add + ModDown.
+int praghip_enc0_evaluate_device_batch(praghip_enc0_plan* p, const uint64_t* samples, uint64_t* output, size_t count,
+                                       void* stream) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
+  if (count == 0) return PRAGHIP_OK;
+  if (!samples || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (count > p->batch_cap) return fail(PRAGHIP_E_SHAPE, "E_ENC0_BATCH");
+  if ((reinterpret_cast<uintptr_t>(samples) | reinterpret_cast<uintptr_t>(output)) & 15)
+    return fail(PRAGHIP_E_ARGUMENT, "E_ENC0_ALIGNMENT");
+  const size_t n = size_t(1) << p->log_n, K = p->K, sample_words = 3 * K * n;
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < K; ++i) m[i] = barrett_of(p->host_q[i]);
+  const hipStream_t s = pick(stream);
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  // u of every encryption: rows of K N words, sample_words apart
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(p->bu, K * n * 8, samples, sample_words * 8, K * n * 8, count, hipMemcpyDeviceToDevice, s);
+  if (e == hipSuccess) e = launch_ntt(false, p->bu, count * K, p->d, s);
+  if (e == hipSuccess)
+    e = launch_token_mac(p->pk, p->bu, p->bprod, count, 1, 2 * K, int(p->log_n), m, int(K), s);
+  if (e == hipSuccess) e = launch_ntt(true, p->bprod, count * 2 * K, p->d, s);
+  if (e == hipSuccess) e = launch_enc0_moddown(p->bprod, samples + K * n, output, p->kc, s, count, sample_words);
+  if (e != hipSuccess) return enc0_failure(p, e, "evaluate_device_batch");
   return PRAGHIP_OK;
 }
 

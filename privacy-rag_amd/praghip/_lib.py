@@ -76,12 +76,16 @@ SIGNATURES = {
     "praghip_matrix_plan_create": (i32, [i32, vp, sz, u32, vp, sz, pp]),
     "praghip_matrix_evaluate": (i32, [vp, vp, vp, vp, sz]),
     "praghip_matrix_evaluate_device": (i32, [vp, vp, vp, vp]),
+    "praghip_matrix_reserve": (i32, [vp, sz]),
+    "praghip_matrix_evaluate_device_batch": (i32, [vp, vp, vp, sz, vp]),
     "praghip_matrix_device_bytes": (sz, [vp]),
     "praghip_matrix_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_matrix_destroy": (None, [vp]),
     "praghip_enc0_plan_create": (i32, [i32, vp, sz, u32, vp, pp]),
     "praghip_enc0_evaluate": (i32, [vp, vp, vp]),
     "praghip_enc0_evaluate_device": (i32, [vp, vp, vp, vp]),
+    "praghip_enc0_reserve": (i32, [vp, sz]),
+    "praghip_enc0_evaluate_device_batch": (i32, [vp, vp, vp, sz, vp]),
     "praghip_enc0_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_enc0_destroy": (None, [vp]),
     "praghip_token_plan_create": (i32, [i32, vp, sz, u32, sz, sz, sz, sz, vp, pp]),

@@ -6,7 +6,7 @@ import ctypes
 
 import numpy as np
 
-from ._lib import Cleanup, check, lib
+from ._lib import Cleanup, check, lib, shape_error
 from ._util import dev_ptr, host_u64, stream_handle, u64_dtypes
 
 
@@ -53,6 +53,21 @@ class Matrix:
                                                    stream_handle(stream)))
         return out
 
+    def reserve(self, groups: int):
+        """Allocates the scratch of evaluate_device_batch for up to `groups` evaluations (once)."""
+        check(lib().praghip_matrix_reserve(self._h, groups))
+
+    def evaluate_device_batch(self, rings, out, stream=None):
+        """rings: GPU [groups][blocks][2^log_n] words below 2^59 (not checked);
+        out: GPU [groups][2][P][2^log_n]."""
+        n = 1 << self.log_n
+        groups = rings.numel() // (self.blocks * n)
+        if groups * self.blocks * n != rings.numel() or out.numel() != groups * 2 * len(self.q) * n:
+            raise shape_error("MATRIX_GPU_SHAPE")
+        check(lib().praghip_matrix_evaluate_device_batch(self._h, dev_ptr(rings, u64_dtypes()),
+                                                         dev_ptr(out, u64_dtypes()), groups, stream_handle(stream)))
+        return out
+
     def device_bytes(self) -> int:
         return int(lib().praghip_matrix_device_bytes(self._h))
 
@@ -95,6 +110,20 @@ class PublicZero:
     def evaluate_device(self, samples, out, stream=None):
         check(lib().praghip_enc0_evaluate_device(self._h, dev_ptr(samples, u64_dtypes()), dev_ptr(out, u64_dtypes()),
                                                  stream_handle(stream)))
+        return out
+
+    def reserve(self, count: int):
+        """Allocates the scratch of evaluate_device_batch for up to `count` encryptions (once)."""
+        check(lib().praghip_enc0_reserve(self._h, count))
+
+    def evaluate_device_batch(self, samples, out, stream=None):
+        """samples: GPU [count][3][K][N] (not checked); out: GPU [count][2][K-1][N]."""
+        K, n = len(self.q), 1 << self.log_n
+        count = samples.numel() // (3 * K * n)
+        if count * 3 * K * n != samples.numel() or out.numel() != count * 2 * (K - 1) * n:
+            raise shape_error("E_SWITCH_SHAPE")
+        check(lib().praghip_enc0_evaluate_device_batch(self._h, dev_ptr(samples, u64_dtypes()),
+                                                       dev_ptr(out, u64_dtypes()), count, stream_handle(stream)))
         return out
 
     def close(self) -> Cleanup:

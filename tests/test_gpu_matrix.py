@@ -101,3 +101,72 @@ def test_enc0(gpu, primes):
     assert c.closed and c.wipe_synchronized_bytes == c.freed_bytes > 0
     with pytest.raises(praghip.PraghipError, match="E_SWITCH_CLOSED"):
         z.evaluate(samples)
+
+
+@pytest.mark.parametrize("log_n,blocks,groups", [(14, 3, 5), (12, 2, 9)])
+def test_matrix_batch(gpu, log_n, blocks, groups):
+    """evaluate_device_batch: `groups` evaluations in one call against the
+    per-evaluation entry point and the oracle (ragged last group of the
+    4-column product tiles)."""
+    import torch
+    print(f"[matrix-batch] log_n={log_n} blocks={blocks} groups={groups}", flush=True)
+    n = 1 << log_n
+    q = cf.LOCKED_PRIMES[:6] if log_n == 14 else cf.primes_below(50, 2 * n, 6)
+    ct = oracle.fill_residues(blocks * 2 * 6, n, q, 500 + blocks).reshape(blocks, 2, 6, n)
+    rings = oracle.fill_u64(groups * blocks * n, 501).reshape(groups, blocks, n) & np.uint64(T59)
+    rings[-1, 0, :3] = [T59, 0, 1 << 58]
+    m = praghip.Matrix(q, log_n, ct)
+    m.reserve(groups)
+    out = to_dev(np.zeros((groups, 2, 6, n), dtype=np.uint64))
+    m.evaluate_device_batch(to_dev(rings), out)
+    one = to_dev(np.zeros((2, 6, n), dtype=np.uint64))
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    for g in range(groups):
+        m.evaluate_device(to_dev(rings[g]), one)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got[g], from_dev(one), err_msg=f"group {g}")
+    for g in (0, groups - 1):
+        np.testing.assert_array_equal(got[g], oracle.matrix_product(ct, rings[g], q, log_n), err_msg=f"oracle {g}")
+    # a smaller batch on the same scratch, then the limits
+    m.evaluate_device_batch(to_dev(rings[:2]), out[:2])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(out[:2]), got[:2])
+    with pytest.raises(praghip.PraghipError, match="MATRIX_GPU_BATCH"):
+        m.evaluate_device_batch(to_dev(np.concatenate([rings, rings[:1]])), to_dev(np.zeros((groups + 1, 2, 6, n),
+                                                                                                 dtype=np.uint64)))
+    with pytest.raises(praghip.PraghipError, match="MATRIX_GPU_BATCH_RESERVED"):
+        m.reserve(groups + 1)
+    m.reserve(1)  # within the reserved count: no change
+    m.close()
+
+
+def test_enc0_batch(gpu):
+    """evaluate_device_batch: several encryptions in one call against the
+    per-encryption entry point and the oracle."""
+    import torch
+    print("[enc0-batch]", flush=True)
+    log_n, n, count = 14, 1 << 14, 6
+    q = cf.primes_below(50, 2 * n, 6) + cf.primes_below(60, 2 * n, 1)
+    pk = oracle.fill_residues(2 * len(q), n, q, 600).reshape(2, len(q), n)
+    z = praghip.PublicZero(q, log_n, pk)
+    z.reserve(count)
+    samples = np.stack([_enc0_samples(q, n, 610 + 10 * e) for e in range(count)])
+    out = to_dev(np.zeros((count, 2, len(q) - 1, n), dtype=np.uint64))
+    z.evaluate_device_batch(to_dev(samples), out)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    one = to_dev(np.zeros((2, len(q) - 1, n), dtype=np.uint64))
+    for e in range(count):
+        z.evaluate_device(to_dev(samples[e]), one)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got[e], from_dev(one), err_msg=f"encryption {e}")
+    for e in (0, count - 1):
+        np.testing.assert_array_equal(got[e], oracle.enc0(samples[e], pk, q, log_n), err_msg=f"oracle {e}")
+    with pytest.raises(praghip.PraghipError, match="E_ENC0_BATCH"):
+        z.evaluate_device_batch(to_dev(np.concatenate([samples, samples[:1]])),
+                                to_dev(np.zeros((count + 1, 2, len(q) - 1, n), dtype=np.uint64)))
+    with pytest.raises(praghip.PraghipError, match="E_ENC0_BATCH_RESERVED"):
+        z.reserve(count + 1)
+    c = z.close()
+    assert c.closed and c.wipe_synchronized_bytes == c.freed_bytes > 0
