@@ -489,9 +489,10 @@ struct praghip_switch_plan {
   NttDevice d;
   KsConst kc{};
   KsConst* kc_dev = nullptr;
-  uint64_t *key = nullptr, *acc = nullptr, *prod = nullptr, *in = nullptr, *out = nullptr;
+  uint64_t *key = nullptr, *acc = nullptr, *prod = nullptr, *in = nullptr, *out = nullptr, *inter = nullptr;
   unsigned* queue = nullptr;
   unsigned acc_slots = 0;
+  size_t inter_cts = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev[4] = {};
   praghip_timing timing{};
@@ -606,6 +607,10 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
   if (e == hipSuccess) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, max_batch * 2 * K * n * 8, true);
+  if (e == hipSuccess && keyswitch_rows_supported(p->kc)) {
+    p->inter_cts = std::min(max_batch, kKsRowsChunk);
+    e = p->buf.alloc((void**)&p->inter, p->inter_cts * dnum * K * n * 8, true);
+  }
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->in, 2 * L * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->out, 2 * L * n * 8, true);
   if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
@@ -631,6 +636,8 @@ static hipError_t keyswitch_chunks(praghip_switch_plan* p, const uint64_t* in, u
     a.prod = p->prod;
     a.galois_inv = ginv;
     a.queue = p->queue;
+    a.inter = p->inter;
+    a.inter_cts = p->inter_cts;
     const hipError_t e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);
     if (e != hipSuccess) return e;
   }

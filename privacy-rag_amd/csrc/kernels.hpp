@@ -57,6 +57,8 @@ struct KsArgs {
   size_t batch;
   uint32_t galois_inv;   // g^-1 mod 2N (1 = identity)
   unsigned* queue;       // scratch [kQueueWords], zero before the first launch (the kernel leaves it zero)
+  uint64_t* inter = nullptr;  // scratch [inter_cts][dnum][K][N]: expanded digits of the three-phase path
+  size_t inter_cts = 0;       // ciphertexts per three-phase chunk (0: whole-limb path only)
 };
 // Work-queue counters of the fused keyswitch: one ticket per XCD group, then
 // the count of finished workgroups.
@@ -127,5 +129,13 @@ hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsCons
 // Workgroups of the fused keyswitch kernel for 2^log_n (the acc slots a plan
 // allocates); 0 for an unsupported size.
 unsigned ks_acc_slots(int log_n);
+// Three-phase keyswitch (columns, rows, columns) for N = 16384 with digits of
+// equal size 1..3; hipErrorNotSupported for any other shape or without the
+// `inter` scratch.  launch_keyswitch takes it when it applies.
+bool keyswitch_rows_supported(const KsConst& kc);
+hipError_t launch_keyswitch_rows(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
+                                 hipStream_t s);
+// Ciphertexts per three-phase chunk a plan sizes its `inter` scratch for.
+constexpr size_t kKsRowsChunk = 64;
 
 }  // namespace praghip

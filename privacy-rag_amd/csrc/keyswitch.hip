@@ -426,6 +426,7 @@ static hipError_t launch_fused_n(KsFused f, hipStream_t s) {
 hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
                             hipStream_t s) {
   if (a.batch == 0) return hipSuccess;
+  if (a.inter && keyswitch_rows_supported(kc)) return launch_keyswitch_rows(a, kc_dev, kc, d, s);
   const size_t n = size_t(1) << kc.log_n;
   KsFused f;
   f.in = a.in;

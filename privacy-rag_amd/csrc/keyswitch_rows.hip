@@ -1,0 +1,610 @@
+// Keyswitch at N = 16384 in three phases (Switch::evaluate, switch.cu:113-125):
+// the same radix-2 stage sequence as the whole-limb path, split where a
+// transform changes from stride-1024 columns to contiguous 1024-coefficient
+// rows, so every phase runs at high occupancy instead of one limb per CU.
+//
+//   A  columns  ModUp of digit j to every key prime t, then forward stages
+//               0-3 (gaps 8192..1024): thread c holds coefficients
+//               c + 1024 k, k = 0..15, and every twiddle is the same for all
+//               threads.  Out: E[b][j][t][N] (lazy, per-policy form).
+//   B  rows     one wave per (ciphertext, prime t, row r): forward stages
+//               4-13 of each digit's row, the key product summed over the
+//               digits in registers, inverse stages 0-9 of both sums.
+//               Out: the products' rows, [b][2][K][N] (lazy).
+//   C  columns  inverse stages 10-13 (N^-1 folded into the last) of both
+//               components on every prime, then ModDown by the special prime
+//               and the c0 term (switch.cu:74-82).
+//
+// Each phase keeps the stage order, the butterflies and the re-centring
+// points of the whole-limb transform, so the values - and the canonical
+// result - are the same.  E and the products pass through HBM (or the last
+// level cache), about twice the algorithmic bytes; the ciphertexts go in
+// chunks so E of one chunk is re-read while it is still cached.
+#include "kernels.hpp"
+#include "ntt_core.hpp"
+
+namespace praghip {
+
+namespace {
+
+constexpr int kLog = 14;                 // N = 16384
+constexpr int kRowLog = 10;              // rows of 1024
+constexpr unsigned kN = 1u << kLog;
+constexpr unsigned kCols = 1u << kRowLog;  // columns of stride 1024
+constexpr unsigned kRowLds = (1u << kRowLog) + (1u << kRowLog) / 16;  // padded LDS words per wave
+
+struct KsRows {
+  const uint64_t* in;   // [batch][2][L][N]
+  uint64_t* out;        // [batch][2][L][N]
+  const uint64_t* key;  // [dnum][2][K][N] per key
+  size_t key_stride;
+  unsigned key_group;
+  uint64_t* e;          // [chunk][dnum][K][N]
+  uint64_t* prod;       // [batch][2][K][N]
+  const KsConst* kc;
+  const NttPrime* primes;
+  const ulonglong2* tw_fwd_u;
+  const ulonglong2* tw_inv_u;
+  const double* tw_fwd_f;
+  const double* tw_inv_f;
+  uint32_t ginv;
+  int data_f64;     // every data prime below 2^50: data primes take the float path
+  int moddown_f64;  // every data prime in (2^32, 2^50): ModDown in FP64 too
+  unsigned b0, cts;  // chunk: ciphertexts b0 .. b0 + cts - 1
+};
+
+__device__ __forceinline__ uint64_t bits_of(double x) { return (uint64_t)__double_as_longlong(x); }
+__device__ __forceinline__ double double_of(uint64_t x) { return __longlong_as_double((long long)x); }
+
+__device__ __forceinline__ uint64_t gather(const uint64_t* __restrict__ limb, unsigned k, uint32_t ginv, uint64_t q) {
+  const unsigned i = (k * ginv) & (2 * kN - 1);
+  const uint64_t v = limb[i & (kN - 1)];
+  return ((i >> kLog) && v) ? q - v : v;
+}
+
+// Stored form of a policy value: doubles by their bits, integers as they are.
+template <class A>
+__device__ __forceinline__ uint64_t store_form(typename A::T x) {
+  if constexpr (std::is_same<typename A::T, double>::value)
+    return bits_of(x);
+  else
+    return x;
+}
+template <class A>
+__device__ __forceinline__ typename A::T load_form(uint64_t x) {
+  if constexpr (std::is_same<typename A::T, double>::value)
+    return double_of(x);
+  else
+    return x;
+}
+
+template <class A>
+__device__ __forceinline__ const typename A::TW* fwd_table(const KsRows& f, int t) {
+  if constexpr (std::is_same<typename A::T, double>::value)
+    return f.tw_fwd_f + (size_t(t) << kLog);
+  else
+    return f.tw_fwd_u + (size_t(t) << kLog);
+}
+template <class A>
+__device__ __forceinline__ const typename A::TW* inv_table(const KsRows& f, int t) {
+  if constexpr (std::is_same<typename A::T, double>::value)
+    return f.tw_inv_f + (size_t(t) << kLog);
+  else
+    return f.tw_inv_u + (size_t(t) << kLog);
+}
+
+// ------------------------------------------------------------------ phase A
+// Waves per SIMD the column kernels are compiled for: the float path fits
+// three, the integer path's 64-bit products need the registers of two.
+template <class A>
+constexpr int kColWaves() {
+  return std::is_same<typename A::T, double>::value ? 3 : 2;
+}
+
+// Twiddles of forward stages 0-3 in the order fwd_pass consumes them: one
+// group per stage (stage s uses fwd[2^s + k], k < 2^s), i.e. fwd[1..15].
+template <class A>
+__device__ __forceinline__ void top_fwd(typename A::T (&v)[kE], const typename A::TW* __restrict__ tab, const A& ar) {
+  typename A::TW w[pass_twiddles<kLogE>()];
+#pragma unroll
+  for (int n = 0; n < pass_twiddles<kLogE>(); ++n) w[n] = tab[1 + n];
+  fwd_pass<kLog, kLog - kLogE, kLogE>(v, w, ar, [] {});
+}
+
+// Modup of one target for the float path: y holds [x_i (Q_j/q_i)^-1]_{q_i}
+// for the digit's primes.
+template <int D>
+__device__ __forceinline__ void cols_target_f64(double (&v)[kE], const uint64_t (&y)[D][kE], const KsConst& kc,
+                                                int lo, int t, const NttPrime& pt) {
+#pragma unroll
+  for (int k = 0; k < kE; ++k) v[k] = 0.0;
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const double hf = double(kc.hat[lo + d][t].w), hfq = hf * pt.qinv;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) v[k] += mul_f64(ArF64::from_u64(y[d][k]), hf, hfq, pt.qd);  // |term| < 7q/8
+  }
+#pragma unroll
+  for (int k = 0; k < kE; ++k) v[k] = reduce_f64(v[k], pt.qd, pt.qinv);
+}
+template <int D>
+__device__ __forceinline__ void cols_target_u64(uint64_t (&v)[kE], const uint64_t (&y)[D][kE], const KsConst& kc,
+                                                int lo, int t) {
+  const uint64_t qt = kc.q[t], qt2 = 2 * qt;
+#pragma unroll
+  for (int k = 0; k < kE; ++k) v[k] = 0;
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const Shoup hf = kc.hat[lo + d][t];
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+      const uint64_t a = v[k] + mul_shoup_lazy(y[d][k], hf.w, hf.wq, qt);  // [0, 4 q_t)
+      v[k] = a >= qt2 ? a - qt2 : a;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kE; ++k) v[k] = v[k] >= qt ? v[k] - qt : v[k];
+}
+
+// y = [x_i (Q_j/q_i)^-1]_{q_i} for the digit's primes at this thread's
+// coefficients, by the policy's arithmetic (exact either way).
+template <int D, class A>
+__device__ __forceinline__ void digit_factors(uint64_t (&y)[D][kE], const KsRows& f, const KsConst& kc,
+                                              const uint64_t* c1, int lo, unsigned c) {
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int i = lo + d;
+    const uint64_t qi = kc.q[i];
+    const Shoup ih = kc.inv_hat[i];
+    const uint64_t* x = c1 + (size_t(i) << kLog);
+    if constexpr (std::is_same<typename A::T, double>::value) {
+      const NttPrime pi = f.primes[i];
+      const double w = double(ih.w), wq = w * pi.qinv;
+#pragma unroll
+      for (int k = 0; k < kE; ++k) {
+        const double v = ArF64::from_u64(gather(x, c + (unsigned(k) << kRowLog), f.ginv, qi));
+        y[d][k] = (uint64_t)canon_f64(mul_f64(v, w, wq, pi.qd), pi.qd);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kE; ++k) y[d][k] = mul_shoup(gather(x, c + (unsigned(k) << kRowLog), f.ginv, qi), ih.w, ih.wq, qi);
+    }
+  }
+}
+
+// Targets per column-forward thread: the digit factors y are computed once
+// for G targets.
+template <class A>
+constexpr unsigned kColTargets() {
+  return std::is_same<typename A::T, double>::value ? 3u : 1u;
+}
+
+// One thread per (ciphertext, digit, group of up to G targets, column), for
+// the targets t_lo .. t_lo + t_n - 1 of one arithmetic policy (A = ArF64Lean:
+// float-path data primes; ArU64: the integer-path primes); digits of exactly
+// D primes.
+template <int D, class A, unsigned G>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
+    ks_cols_fwd_kernel(KsRows f, unsigned t_lo, unsigned t_n) {
+  using T = typename A::T;
+  const KsConst& kc = *f.kc;
+  const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K), L = unsigned(kc.L);
+  const unsigned groups = (t_n + G - 1) / G;
+  const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= f.cts * dnum * groups * kCols) return;
+  const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;  // w is uniform per wave
+  const unsigned g = w % groups, j = (w / groups) % dnum, bl = w / (groups * dnum), b = f.b0 + bl;
+  const int lo = kc.dig_lo[j];
+  const uint64_t* c1 = f.in + ((size_t(b) * 2 + 1) * L << kLog);
+  uint64_t y[D][kE];
+  const unsigned t_first = t_lo + g * G, t_end = t_lo + (g * G + G < t_n ? g * G + G : t_n);
+  if (G > 1) digit_factors<D, A>(y, f, kc, c1, lo, c);
+  for (unsigned t = t_first; t < t_end; ++t) {
+    const NttPrime pt = f.primes[t];
+    const A ar(pt);
+    T v[kE];
+    if (int(t) >= lo && int(t) < lo + D) {  // a prime of the digit: its own residues
+#pragma unroll
+      for (int k = 0; k < kE; ++k)
+        v[k] = ar.from_u64(gather(c1 + (size_t(t) << kLog), c + (unsigned(k) << kRowLog), f.ginv, pt.q));
+    } else {
+      if (G == 1) digit_factors<D, A>(y, f, kc, c1, lo, c);
+      if constexpr (std::is_same<T, double>::value)
+        cols_target_f64<D>(v, y, kc, lo, int(t), pt);
+      else
+        cols_target_u64<D>(v, y, kc, lo, int(t));
+    }
+    top_fwd<A>(v, fwd_table<A>(f, int(t)), ar);
+    uint64_t* et = f.e + ((size_t(bl) * dnum + j) * K + t) * kN + c;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) et[unsigned(k) << kRowLog] = store_form<A>(v[k]);
+  }
+}
+
+// ------------------------------------------------------------------ phase B
+// Twiddles of row pass P (a 1024-coefficient transform's pass map, with the
+// row's bits above it): global group index = (row << 10 | local) >> (LO + R).
+template <bool INV, int P, class TW>
+__device__ __forceinline__ void row_twiddles(TW (&w)[pass_twiddles<Passes<kRowLog>::r(INV, P)>()], unsigned lane,
+                                             unsigned row, const TW* __restrict__ tab) {
+  using M = PassMap<kRowLog, INV, P>;
+  constexpr int LO = M::LO, R = M::R, SUB = kE >> R;
+  int n = 0;
+#pragma unroll
+  for (int b = 0; b < SUB; ++b) {
+    const unsigned hi_lane = ((row << kRowLog) | M::elem(lane, b << R)) >> (LO + R);
+    const unsigned hi = M::uniform_groups() ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (!INV) {
+        const int s = kLog - LO - R + i;
+#pragma unroll
+        for (int k = 0; k < (1 << i); ++k) w[n++] = tab[(1u << s) + (hi << i) + k];
+      } else {
+        const int l = LO + i;
+#pragma unroll
+        for (int k = 0; k < (1 << (R - 1 - i)); ++k) w[n++] = tab[kN - (kN >> l) + 1 + (hi << (R - 1 - i)) + k];
+      }
+    }
+  }
+}
+
+template <bool INV, int P, class A>
+__device__ __forceinline__ void row_pass(typename A::T (&v)[kE], unsigned lane, unsigned row,
+                                         const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr) {
+  using S = Passes<kRowLog>;
+  constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
+  typename A::TW w[pass_twiddles<R>()];
+  row_twiddles<INV, P>(w, lane, row, tab);
+  // stage numbers are the N = 16384 transform's: no row stage is the last
+  // inverse stage, and the re-centring points are the whole transform's
+  if constexpr (INV)
+    inv_pass<kLog, LO, R>(v, w, ar, pr, [] {});
+  else
+    fwd_pass<kLog, LO, R>(v, w, ar, [] {});
+}
+
+template <bool INV, class A>
+__device__ __forceinline__ void row_transform(typename A::T (&v)[kE], typename A::T* lds, unsigned lane, unsigned row,
+                                              const typename A::TW* __restrict__ tab, const A& ar,
+                                              const NttPrime& pr) {
+  row_pass<INV, 0>(v, lane, row, tab, ar, pr);
+  exchange<kRowLog, INV, 0>(v, lds, lane);
+  row_pass<INV, 1>(v, lane, row, tab, ar, pr);
+  exchange<kRowLog, INV, 1>(v, lds, lane);
+  row_pass<INV, 2>(v, lane, row, tab, ar, pr);
+}
+
+__device__ __forceinline__ void row_mac_u64(uint64_t (&v)[kE], uint64_t (&a0)[kE], uint64_t (&a1)[kE],
+                                            const uint64_t* __restrict__ k0, const uint64_t* __restrict__ k1,
+                                            unsigned lane, unsigned row, bool first, const ArU64& ar,
+                                            const Barrett& bar) {
+#pragma unroll
+  for (int r = 0; r < kE; r += 2) {
+    const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog>(lane, r);
+    const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+    const ulonglong2 kb = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = r + h;
+      // the transformed digit word meets two key words: one Shoup quotient,
+      // two Shoup products
+      const uint64_t x = ar.to_u64_fwd(v[rr]);
+      const uint64_t xq = shoup_quotient(x, bar);
+      const uint64_t p0 = mul_shoup(h ? ka.y : ka.x, x, xq, ar.q);
+      const uint64_t p1 = mul_shoup(h ? kb.y : kb.x, x, xq, ar.q);
+      a0[rr] = first ? p0 : add_mod(a0[rr], p0, ar.q);
+      a1[rr] = first ? p1 : add_mod(a1[rr], p1, ar.q);
+    }
+    if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <class A>
+__device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t, unsigned row,
+                                         unsigned lane, typename A::T* lds) {
+  using T = typename A::T;
+  const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K);
+  const unsigned b = f.b0 + bl;
+  const NttPrime pr = f.primes[t];
+  const A ar(pr);
+  const typename A::TW* tf = fwd_table<A>(f, int(t));
+  const typename A::TW* ti = inv_table<A>(f, int(t));
+  const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
+  T a0[kE], a1[kE];
+  for (unsigned j = 0; j < dnum; ++j) {
+    const uint64_t* src = f.e + ((size_t(bl) * dnum + j) * K + t) * kN + (row << kRowLog);
+    T v[kE];
+#pragma unroll
+    for (int k = 0; k < kE; ++k) v[k] = load_form<A>(src[fwd_in_index<kRowLog>(lane, k)]);
+    row_transform<false>(v, lds, lane, row, tf, ar, pr);
+    const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << kLog);
+    const uint64_t* k1 = k0 + (size_t(K) << kLog);
+    row_mac_u64(v, a0, a1, k0, k1, lane, row, j == 0, ar, kc.bar[t]);
+    // the next digit's first exchange writes the LDS this digit's last one read
+    __builtin_amdgcn_wave_barrier();
+  }
+  uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
+  row_transform<true>(a0, lds, lane, row, ti, ar, pr);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) pb[inv_out_index<kRowLog>(lane, k)] = store_form<A>(a0[k]);
+  __builtin_amdgcn_wave_barrier();
+  row_transform<true>(a1, lds, lane, row, ti, ar, pr);
+  uint64_t* pc = pb + (size_t(K) << kLog);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) pc[inv_out_index<kRowLog>(lane, k)] = store_form<A>(a1[k]);
+}
+
+// The float-path row item.  (Loading a digit's key words before its forward
+// transform, or the next digit's row before the key product, does not pay:
+// vector loads complete in order, so each pass's twiddle wait also waits for
+// the early loads, and the extra registers spill.)
+__device__ __forceinline__ void row_item_f64(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t, unsigned row,
+                                             unsigned lane, double* lds) {
+  using A = ArF64Lean;
+  const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K);
+  const unsigned b = f.b0 + bl;
+  const NttPrime pr = f.primes[t];
+  const A ar(pr);
+  const double* tf = f.tw_fwd_f + (size_t(t) << kLog);
+  const double* ti = f.tw_inv_f + (size_t(t) << kLog);
+  const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
+  const uint64_t* e0 = f.e + (size_t(bl) * dnum * K + t) * kN + (row << kRowLog);
+  const size_t e_digit = size_t(K) * kN;
+  double a0[kE], a1[kE];
+  for (unsigned j = 0; j < dnum; ++j) {
+    double v[kE];
+#pragma unroll
+    for (int k = 0; k < kE; ++k) v[k] = double_of(e0[j * e_digit + fwd_in_index<kRowLog>(lane, k)]);
+    row_transform<false>(v, lds, lane, row, tf, ar, pr);
+    const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << kLog);
+    const uint64_t* k1 = k0 + (size_t(K) << kLog);
+#pragma unroll
+    for (int r = 0; r < kE; r += 2) {
+      // registers r, r + 1 hold adjacent coefficients after the last forward
+      // pass: one 16-byte load per key limb
+      const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog>(lane, r);
+      const ulonglong2 x = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+      const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // |v| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
+        const double p0 = ar.mul(v[r + h], ArF64::from_u64(h ? x.y : x.x));
+        const double p1 = ar.mul(v[r + h], ArF64::from_u64(h ? y.y : y.x));
+        a0[r + h] = reduce_f64(j ? a0[r + h] + p0 : p0, ar.q, ar.qinv);
+        a1[r + h] = reduce_f64(j ? a1[r + h] + p1 : p1, ar.q, ar.qinv);
+      }
+    }
+    // the next digit's first exchange writes the LDS this digit's last one read
+    __builtin_amdgcn_wave_barrier();
+  }
+  uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
+  row_transform<true>(a0, lds, lane, row, ti, ar, pr);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) pb[inv_out_index<kRowLog>(lane, k)] = bits_of(a0[k]);
+  __builtin_amdgcn_wave_barrier();
+  row_transform<true>(a1, lds, lane, row, ti, ar, pr);
+  uint64_t* pc = pb + (size_t(K) << kLog);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) pc[inv_out_index<kRowLog>(lane, k)] = bits_of(a1[k]);
+}
+
+constexpr unsigned kRowWaves = 4;  // waves (items) per workgroup
+
+// One wave per (ciphertext, prime t, row).  Items [0, u64_items) are the
+// integer-path primes t_u64 .. K - 1 (the special prime, or every prime when
+// a data prime has 50 bits or more) and go first, being the longest; the rest
+// are the float-path data primes 0 .. t_u64 - 1.
+__global__ void __launch_bounds__(64 * kRowWaves) __attribute__((amdgpu_waves_per_eu(2)))
+    ks_rows_kernel(KsRows f, unsigned t_u64) {
+  __shared__ __attribute__((aligned(16))) uint64_t lds_all[kRowWaves * kRowLds];
+  const KsConst& kc = *f.kc;
+  const unsigned K = unsigned(kc.K);
+  const unsigned lane = threadIdx.x & 63u;
+  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const unsigned item = blockIdx.x * kRowWaves + wave;
+  constexpr unsigned rows = kN >> kRowLog;
+  const unsigned n_u64 = K - t_u64, u64_items = f.cts * n_u64 * rows;
+  if (item >= f.cts * K * rows) return;
+  uint64_t* lds = lds_all + wave * kRowLds;
+  if (item < u64_items) {
+    const unsigned row = item % rows, t = t_u64 + (item / rows) % n_u64, bl = item / (rows * n_u64);
+    row_item<ArU64>(f, kc, bl, t, row, lane, lds);
+  } else {
+    const unsigned x = item - u64_items;
+    const unsigned row = x % rows, t = (x / rows) % t_u64, bl = x / (rows * t_u64);
+    row_item_f64(f, kc, bl, t, row, lane, reinterpret_cast<double*>(lds));
+  }
+}
+
+// ------------------------------------------------------------------ phase C
+template <class A>
+__device__ __forceinline__ void top_inv(typename A::T (&v)[kE], const typename A::TW* __restrict__ tab, const A& ar,
+                                        const NttPrime& pr) {
+  // inverse stages 10-13: stage l uses inv[N - (N >> l) + 1 + k], k < 2^(13-l);
+  // stage 13 (one group) takes N^-1 and its twiddle from the prime constants
+  typename A::TW w[pass_twiddles<kLogE>()];
+  int n = 0;
+#pragma unroll
+  for (int i = 0; i < kLogE; ++i) {
+    const int l = kLog - kLogE + i;
+#pragma unroll
+    for (int k = 0; k < (1 << (kLogE - 1 - i)); ++k) {
+      if (l != kLog - 1) w[n] = tab[kN - (kN >> l) + 1 + k];
+      ++n;
+    }
+  }
+  inv_pass<kLog, kLog - kLogE, kLogE>(v, w, ar, pr, [] {});
+}
+
+// Canonical coefficient-form residues of one product limb at column c.
+template <class A>
+__device__ __forceinline__ void column_residues(uint64_t (&x)[kE], const uint64_t* __restrict__ src,
+                                                const typename A::TW* __restrict__ tab, const NttPrime& pr) {
+  const A ar(pr);
+  typename A::T v[kE];
+#pragma unroll
+  for (int k = 0; k < kE; ++k) v[k] = load_form<A>(src[unsigned(k) << kRowLog]);
+  top_inv<A>(v, tab, ar, pr);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) x[k] = ar.to_u64_inv(v[k]);
+}
+
+// Special-prime limbs first: one thread per (ciphertext, component,
+// column) finishes the inverse transform and leaves [P_p + floor(p/2)]_p in
+// place of the limb, the rounding term every data prime's ModDown reads.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) ks_cols_special_kernel(KsRows f) {
+  const KsConst& kc = *f.kc;
+  const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
+  const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= f.cts * 2 * kCols) return;
+  const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;
+  const unsigned comp = w & 1u, b = f.b0 + (w >> 1);
+  uint64_t* pl = f.prod + ((size_t(b) * 2 + comp) * K + L) * kN + c;
+  const uint64_t p = kc.q[L], half = p >> 1;
+  uint64_t last[kE];
+  column_residues<ArU64>(last, pl, f.tw_inv_u + (size_t(L) << kLog), f.primes[L]);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) {
+    const uint64_t x = last[k] + half;
+    pl[unsigned(k) << kRowLog] = x >= p ? x - p : x;
+  }
+}
+
+// Then one thread per (ciphertext, component, data prime, column) finishes
+// that prime's inverse transform (policy A) and applies ModDown (+ c0).
+template <class A>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
+    ks_cols_inv_kernel(KsRows f) {
+  const KsConst& kc = *f.kc;
+  const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
+  const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= f.cts * 2 * L * kCols) return;
+  const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;
+  const unsigned i = w % L, comp = (w / L) & 1u, b = f.b0 + w / (2 * L);
+  const uint64_t* pc = f.prod + ((size_t(b) * 2 + comp) * K << kLog) + c;
+  const uint64_t qi = kc.q[i];
+  const uint64_t* c0 = f.in + ((size_t(b) * 2 * L + i) << kLog);
+  uint64_t* o = f.out + (((size_t(b) * 2 + comp) * L + i) << kLog) + c;
+  if constexpr (std::is_same<typename A::T, double>::value) {
+    if (f.moddown_f64) {
+      // exact FP64 ModDown for 2^32 < q_i < 2^50: last = hi 2^32 + lo gives
+      // [last]_{q_i} = hi 2^32 + lo (mod q_i) with one product, then
+      // (x - [last]_{q_i} + floor(p/2)) p^-1, all centred, canonical at the end
+      const NttPrime pi = f.primes[i];
+      const ArF64 ar(pi);
+      // every operand is loaded before the inverse stages, so the loads of
+      // the rounding term and c0 overlap the arithmetic
+      double v[kE];
+      uint64_t lastv[kE], c0v[kE];
+#pragma unroll
+      for (int k = 0; k < kE; ++k) v[k] = double_of(pc[(size_t(i) << kLog) + (unsigned(k) << kRowLog)]);
+#pragma unroll
+      for (int k = 0; k < kE; ++k) lastv[k] = pc[(size_t(L) << kLog) + (unsigned(k) << kRowLog)];
+#pragma unroll
+      for (int k = 0; k < kE; ++k) c0v[k] = comp == 0 ? gather(c0, c + (unsigned(k) << kRowLog), f.ginv, qi) : 0;
+      top_inv<ArF64>(v, f.tw_inv_f + (size_t(i) << kLog), ar, pi);
+      const double c32 = 4294967296.0, c32q = c32 * pi.qinv;
+      const double ip = double(kc.invp[i].w), ipq = ip * pi.qinv, half = double(kc.half_mod[i]);
+#pragma unroll
+      for (int k = 0; k < kE; ++k) {
+        const uint64_t last = lastv[k];
+        // |red| < 1.9 q, |x| <= q/2 + 1: the factor below stays under 3.4 q
+        const double red = mul_f64(double(last >> 32), c32, c32q, pi.qd) + double(last & 0xffffffffull);
+        double r = mul_f64(reduce_f64(v[k], pi.qd, pi.qinv) - red + half, ip, ipq, pi.qd);  // |r| < 1.8 q
+        r += ArF64::from_u64(c0v[k]);
+        o[unsigned(k) << kRowLog] = ar.to_u64(r);
+      }
+      return;
+    }
+  }
+  uint64_t x[kE];
+  column_residues<A>(x, pc + (size_t(i) << kLog), inv_table<A>(f, int(i)), f.primes[i]);
+#pragma unroll
+  for (int k = 0; k < kE; ++k) {
+    const uint64_t last = pc[(size_t(L) << kLog) + (unsigned(k) << kRowLog)];
+    const uint64_t reduced = mul_shoup(last, 1, kc.one_q[i], qi);  // last mod q_i
+    const uint64_t corr = sub_mod(reduced, kc.half_mod[i], qi);
+    uint64_t val = mul_shoup(sub_mod(x[k], corr, qi), kc.invp[i].w, kc.invp[i].wq, qi);
+    if (comp == 0) val = add_mod(val, gather(c0, c + (unsigned(k) << kRowLog), f.ginv, qi), qi);
+    o[unsigned(k) << kRowLog] = val;
+  }
+}
+
+}  // namespace
+
+// Digit size when every digit has the same number of primes (0 otherwise).
+static int uniform_digit(const KsConst& kc) {
+  const int d = kc.dig_lo[1] - kc.dig_lo[0];
+  for (int j = 1; j < kc.dnum; ++j)
+    if (kc.dig_lo[j + 1] - kc.dig_lo[j] != d) return 0;
+  return d;
+}
+
+template <int D>
+static void launch_cols_fwd(const KsRows& f, unsigned dnum, unsigned t_u64, unsigned K, hipStream_t s) {
+  const auto grid = [&](unsigned t_n, unsigned g) { return dim3((f.cts * dnum * ((t_n + g - 1) / g) * kCols + 255) / 256); };
+  constexpr unsigned GU = kColTargets<ArU64>(), GF = kColTargets<ArF64Lean>();
+  hipLaunchKernelGGL((ks_cols_fwd_kernel<D, ArU64, GU>), grid(K - t_u64, GU), dim3(256), 0, s, f, t_u64, K - t_u64);
+  if (t_u64) hipLaunchKernelGGL((ks_cols_fwd_kernel<D, ArF64Lean, GF>), grid(t_u64, GF), dim3(256), 0, s, f, 0u, t_u64);
+}
+
+bool keyswitch_rows_supported(const KsConst& kc) {
+  const int d = uniform_digit(kc);
+  return kc.log_n == kLog && d >= 1 && d <= 3;
+}
+
+hipError_t launch_keyswitch_rows(const KsArgs& a, const KsConst* kc_dev, const KsConst& kc, const NttDevice& d,
+                                 hipStream_t s) {
+  const int dig = uniform_digit(kc);
+  if (kc.log_n != kLog || dig < 1 || dig > 3 || !a.inter || a.inter_cts == 0) return hipErrorNotSupported;
+  KsRows f;
+  f.in = a.in;
+  f.out = a.out;
+  f.key = a.key;
+  f.key_stride = a.key_stride;
+  f.key_group = unsigned(a.key_group ? a.key_group : 1);
+  f.e = a.inter;
+  f.prod = a.prod;
+  f.kc = kc_dev;
+  f.primes = d.primes;
+  f.tw_fwd_u = d.tw_fwd_u;
+  f.tw_inv_u = d.tw_inv_u;
+  f.tw_fwd_f = d.tw_fwd_f;
+  f.tw_inv_f = d.tw_inv_f;
+  f.ginv = a.galois_inv;
+  f.data_f64 = 1;
+  f.moddown_f64 = 1;
+  for (int i = 0; i < kc.L; ++i) {
+    f.data_f64 &= kc.q[i] < (1ull << 50) ? 1 : 0;
+    f.moddown_f64 &= (kc.q[i] < (1ull << 50) && kc.q[i] > (1ull << 32)) ? 1 : 0;
+  }
+  const unsigned K = unsigned(kc.K), L = unsigned(kc.L), dnum = unsigned(kc.dnum), rows = kN >> kRowLog;
+  for (size_t b0 = 0; b0 < a.batch; b0 += a.inter_cts) {
+    f.b0 = unsigned(b0);
+    f.cts = unsigned(std::min<size_t>(a.inter_cts, a.batch - b0));
+    // the integer-path primes t_u64 .. K - 1 (the special prime, or every
+    // prime when a data prime has 50 bits or more), the float-path data
+    // primes below t_u64
+    const unsigned t_u64 = f.data_f64 ? L : 0;
+    switch (dig) {
+      case 1: launch_cols_fwd<1>(f, dnum, t_u64, K, s); break;
+      case 2: launch_cols_fwd<2>(f, dnum, t_u64, K, s); break;
+      default: launch_cols_fwd<3>(f, dnum, t_u64, K, s); break;
+    }
+    const unsigned items = f.cts * K * rows;
+    hipLaunchKernelGGL(ks_rows_kernel, dim3((items + kRowWaves - 1) / kRowWaves), dim3(64 * kRowWaves), 0, s, f,
+                       t_u64);
+    hipLaunchKernelGGL(ks_cols_special_kernel, dim3((f.cts * 2 * kCols + 255) / 256), dim3(256), 0, s, f);
+    const dim3 c_grid((f.cts * 2 * L * kCols + 255) / 256);
+    if (f.data_f64)
+      hipLaunchKernelGGL(ks_cols_inv_kernel<ArF64>, c_grid, dim3(256), 0, s, f);
+    else
+      hipLaunchKernelGGL(ks_cols_inv_kernel<ArU64>, c_grid, dim3(256), 0, s, f);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace praghip

@@ -395,8 +395,9 @@ struct praghip_pack_plan {
   NttDevice d;
   KsConst kc{};
   KsConst* kc_dev = nullptr;
-  uint64_t *keys = nullptr, *work = nullptr, *ksout = nullptr, *prod = nullptr, *acc = nullptr;
+  uint64_t *keys = nullptr, *work = nullptr, *ksout = nullptr, *prod = nullptr, *acc = nullptr, *inter = nullptr;
   uint64_t *host_in = nullptr, *host_out = nullptr;
+  size_t inter_cts = 0;
   unsigned* queue = nullptr;
   unsigned acc_slots = 0;
   size_t merges = 0;
@@ -447,6 +448,8 @@ hipError_t pack_run(praghip_pack_plan* p, const uint64_t* left, const uint64_t* 
     a.batch = 2 * c;
     a.galois_inv = 1;  // the Galois map is applied by the prepare kernel
     a.queue = p->queue;
+    a.inter = p->inter;
+    a.inter_cts = p->inter_cts;
     e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);
     if (e == hipSuccess) e = launch_pack_finish(p->ksout, p->ksout + c * ct, out + c0 * ct, c, pl, int(p->log_n), s);
   }
@@ -501,6 +504,10 @@ int praghip_pack_plan_create(int device, const uint64_t* q, size_t data_primes, 
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->work, 2 * max_pairs * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->ksout, 2 * max_pairs * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, 2 * max_pairs * 2 * K * n * 8, true);
+  if (e == hipSuccess && keyswitch_rows_supported(p->kc)) {
+    p->inter_cts = std::min(2 * max_pairs, kKsRowsChunk);
+    e = p->buf.alloc((void**)&p->inter, p->inter_cts * dnum * K * n * 8, true);
+  }
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->host_in, 2 * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->host_out, ct * 8, true);
   if (e == hipSuccess) e = hipStreamSynchronize(p->stream);

@@ -11,7 +11,7 @@ CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
 OBJ = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libpraghip.so")
-SOURCES = ["ntt.hip", "keyswitch.hip", "gemm.hip", "elementwise.hip", "shares.hip", "token.hip", "api.cpp",
+SOURCES = ["ntt.hip", "keyswitch.hip", "keyswitch_rows.hip", "gemm.hip", "elementwise.hip", "shares.hip", "token.hip", "api.cpp",
            "plans.cpp", "weights.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Wall", "-Wno-unused-function",
