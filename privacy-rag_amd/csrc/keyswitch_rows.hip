@@ -173,10 +173,11 @@ __device__ __forceinline__ void digit_factors(uint64_t (&y)[D][kE], const KsRows
 }
 
 // Targets per column-forward thread: the digit factors y are computed once
-// for G targets.
+// for G targets (all six float-path data primes at L = 6: c1 is then read
+// once per digit, instead of once per target group on different XCDs).
 template <class A>
 constexpr unsigned kColTargets() {
-  return std::is_same<typename A::T, double>::value ? 3u : 1u;
+  return std::is_same<typename A::T, double>::value ? 6u : 1u;
 }
 
 // One thread per (ciphertext, digit, group of up to G targets, column), for
@@ -184,13 +185,19 @@ constexpr unsigned kColTargets() {
 // float-path data primes; ArU64: the integer-path primes); digits of exactly
 // D primes.
 template <int D, class A, unsigned G>
+__device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, unsigned t_n, unsigned blk);
+template <int D, class A, unsigned G>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
     ks_cols_fwd_kernel(KsRows f, unsigned t_lo, unsigned t_n) {
+  cols_fwd_body<D, A, G>(f, t_lo, t_n, blockIdx.x);
+}
+template <int D, class A, unsigned G>
+__device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, unsigned t_n, unsigned blk) {
   using T = typename A::T;
   const KsConst& kc = *f.kc;
   const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K), L = unsigned(kc.L);
   const unsigned groups = (t_n + G - 1) / G;
-  const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const unsigned gid = blk * blockDim.x + threadIdx.x;
   if (gid >= f.cts * dnum * groups * kCols) return;
   const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;  // w is uniform per wave
   const unsigned g = w % groups, j = (w / groups) % dnum, bl = w / (groups * dnum), b = f.b0 + bl;
@@ -219,6 +226,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWa
 #pragma unroll
     for (int k = 0; k < kE; ++k) et[unsigned(k) << kRowLog] = store_form<A>(v[k]);
   }
+}
+
+// Both policies in one launch when both are present: the first nu blocks
+// take the integer-path primes t_u64 .. t_u64 + n_u64 - 1, the rest the
+// float-path data primes, so the special prime's 64-bit work overlaps the
+// float targets instead of running after them.
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+    ks_cols_fwd_both(KsRows f, unsigned t_u64, unsigned n_u64, unsigned nu) {
+  if (blockIdx.x < nu) cols_fwd_body<D, ArU64, 1>(f, t_u64, n_u64, blockIdx.x);
+  else cols_fwd_body<D, ArF64Lean, kColTargets<ArF64Lean>()>(f, 0u, t_u64, blockIdx.x - nu);
 }
 
 // ------------------------------------------------------------------ phase B
@@ -268,11 +286,31 @@ template <bool INV, class A>
 __device__ __forceinline__ void row_transform(typename A::T (&v)[kE], typename A::T* lds, unsigned lane, unsigned row,
                                               const typename A::TW* __restrict__ tab, const A& ar,
                                               const NttPrime& pr) {
-  row_pass<INV, 0>(v, lane, row, tab, ar, pr);
-  exchange<kRowLog, INV, 0>(v, lds, lane);
-  row_pass<INV, 1>(v, lane, row, tab, ar, pr);
-  exchange<kRowLog, INV, 1>(v, lds, lane);
-  row_pass<INV, 2>(v, lane, row, tab, ar, pr);
+  if constexpr (A::kAhead) {
+    // each pass's twiddles are loaded halfway through the pass before
+    using S = Passes<kRowLog>;
+    using TW = typename A::TW;
+    TW w0[pass_twiddles<S::r(INV, 0)>()], w1[pass_twiddles<S::r(INV, 1)>()], w2[pass_twiddles<S::r(INV, 2)>()];
+    row_twiddles<INV, 0>(w0, lane, row, tab);
+    const auto pass = [&](auto p, auto& w, auto&& mid) {
+      constexpr int P = decltype(p)::value, LO = S::lo(INV, P), R = S::r(INV, P);
+      if constexpr (INV)
+        inv_pass<kLog, LO, R>(v, w, ar, pr, mid);
+      else
+        fwd_pass<kLog, LO, R>(v, w, ar, mid);
+    };
+    pass(std::integral_constant<int, 0>{}, w0, [&] { row_twiddles<INV, 1>(w1, lane, row, tab); });
+    exchange<kRowLog, INV, 0>(v, lds, lane);
+    pass(std::integral_constant<int, 1>{}, w1, [&] { row_twiddles<INV, 2>(w2, lane, row, tab); });
+    exchange<kRowLog, INV, 1>(v, lds, lane);
+    pass(std::integral_constant<int, 2>{}, w2, [] {});
+  } else {
+    row_pass<INV, 0>(v, lane, row, tab, ar, pr);
+    exchange<kRowLog, INV, 0>(v, lds, lane);
+    row_pass<INV, 1>(v, lane, row, tab, ar, pr);
+    exchange<kRowLog, INV, 1>(v, lds, lane);
+    row_pass<INV, 2>(v, lane, row, tab, ar, pr);
+  }
 }
 
 __device__ __forceinline__ void row_mac_u64(uint64_t (&v)[kE], uint64_t (&a0)[kE], uint64_t (&a1)[kE],
@@ -335,13 +373,14 @@ __device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, uns
   for (int k = 0; k < kE; ++k) pc[inv_out_index<kRowLog>(lane, k)] = store_form<A>(a1[k]);
 }
 
-// The float-path row item.  (Loading a digit's key words before its forward
+// The float-path row item (each pass's twiddles loaded halfway through the
+// pass before).  (Loading a digit's key words before its forward
 // transform, or the next digit's row before the key product, does not pay:
 // vector loads complete in order, so each pass's twiddle wait also waits for
 // the early loads, and the extra registers spill.)
 __device__ __forceinline__ void row_item_f64(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t, unsigned row,
                                              unsigned lane, double* lds) {
-  using A = ArF64Lean;
+  using A = ArF64;
   const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K);
   const unsigned b = f.b0 + bl;
   const NttPrime pr = f.primes[t];
@@ -545,8 +584,12 @@ template <int D>
 static void launch_cols_fwd(const KsRows& f, unsigned dnum, unsigned t_u64, unsigned K, hipStream_t s) {
   const auto grid = [&](unsigned t_n, unsigned g) { return dim3((f.cts * dnum * ((t_n + g - 1) / g) * kCols + 255) / 256); };
   constexpr unsigned GU = kColTargets<ArU64>(), GF = kColTargets<ArF64Lean>();
-  hipLaunchKernelGGL((ks_cols_fwd_kernel<D, ArU64, GU>), grid(K - t_u64, GU), dim3(256), 0, s, f, t_u64, K - t_u64);
-  if (t_u64) hipLaunchKernelGGL((ks_cols_fwd_kernel<D, ArF64Lean, GF>), grid(t_u64, GF), dim3(256), 0, s, f, 0u, t_u64);
+  if (!t_u64) {  // every prime on the integer path
+    hipLaunchKernelGGL((ks_cols_fwd_kernel<D, ArU64, GU>), grid(K, GU), dim3(256), 0, s, f, 0u, K);
+    return;
+  }
+  const unsigned nu = grid(K - t_u64, GU).x, nf = grid(t_u64, GF).x;
+  hipLaunchKernelGGL((ks_cols_fwd_both<D>), dim3(nu + nf), dim3(256), 0, s, f, t_u64, K - t_u64, nu);
 }
 
 bool keyswitch_rows_supported(const KsConst& kc) {
