@@ -115,3 +115,23 @@ def test_switch_errors_and_cleanup(gpu):
     with pytest.raises(praghip.PraghipError) as e:
         praghip.Switch(q, 14, dnum, key=bad_key)
     assert "E_SWITCH_KEY_CANONICAL" in e.value.text
+
+
+def test_keyswitch_rows_chunks(gpu):
+    """A batch of 67 at N=16384 runs as two internal chunks of the three-phase
+    path (64 + 3, the second starting at ciphertext 64) with per-ciphertext
+    keys and a Galois element; spot-checked against the oracle."""
+    import torch
+    q, n, L, dnum, batch = P16384_SWITCH, 16384, 6, 3, 67
+    print("[ks] rows chunks batch=67", flush=True)
+    sw = praghip.Switch(q, 14, dnum, max_batch=batch)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000903).reshape(batch, 2, L, n)
+    keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x5052414700010903).reshape(
+        batch, dnum, 2, L + 1, n)
+    tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
+    sw.keyswitch(tin, tout, keys=to_dev(keys), key_stride=sw.key_words, galois=3)
+    torch.cuda.synchronize()
+    got = from_dev(tout)
+    for b in (0, 63, 64, 66):
+        np.testing.assert_array_equal(got[b], oracle.keyswitch(ct[b:b + 1], keys[b], q, dnum, 14, 3)[0],
+                                      err_msg=f"ciphertext {b}")
