@@ -11,15 +11,17 @@
 //               4-13 of each digit's row, the key product summed over the
 //               digits in registers, inverse stages 0-9 of both sums.
 //               Out: the products' rows, [b][2][K][N] (lazy).
-//   C  columns  inverse stages 10-13 (N^-1 folded into the last) of both
-//               components on every prime, then ModDown by the special prime
-//               and the c0 term (switch.cu:74-82).
+//   C  columns  inverse stages 10-13 (N^-1 folded into the last): first the
+//               special prime's, leaving the ModDown rounding term in place,
+//               then every data prime's with ModDown and the c0 term
+//               (switch.cu:74-82).
 //
 // Each phase keeps the stage order, the butterflies and the re-centring
 // points of the whole-limb transform, so the values - and the canonical
-// result - are the same.  E and the products pass through HBM (or the last
-// level cache), about twice the algorithmic bytes; the ciphertexts go in
-// chunks so E of one chunk is re-read while it is still cached.
+// result - are the same.  E and the products pass through HBM, about twice
+// the algorithmic bytes.  The ciphertexts go in chunks of up to 64 (the
+// scratch a plan sizes E for); smaller chunks, which would keep E in the
+// last-level cache, leave too few workgroups per launch and are slower.
 #include "kernels.hpp"
 #include "ntt_core.hpp"
 
@@ -185,13 +187,6 @@ constexpr unsigned kColTargets() {
 // float-path data primes; ArU64: the integer-path primes); digits of exactly
 // D primes.
 template <int D, class A, unsigned G>
-__device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, unsigned t_n, unsigned blk);
-template <int D, class A, unsigned G>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
-    ks_cols_fwd_kernel(KsRows f, unsigned t_lo, unsigned t_n) {
-  cols_fwd_body<D, A, G>(f, t_lo, t_n, blockIdx.x);
-}
-template <int D, class A, unsigned G>
 __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, unsigned t_n, unsigned blk) {
   using T = typename A::T;
   const KsConst& kc = *f.kc;
@@ -226,6 +221,13 @@ __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, un
 #pragma unroll
     for (int k = 0; k < kE; ++k) et[unsigned(k) << kRowLog] = store_form<A>(v[k]);
   }
+}
+
+// One policy per launch (every prime on the integer path).
+template <int D, class A, unsigned G>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
+    ks_cols_fwd_kernel(KsRows f, unsigned t_lo, unsigned t_n) {
+  cols_fwd_body<D, A, G>(f, t_lo, t_n, blockIdx.x);
 }
 
 // Both policies in one launch when both are present: the first nu blocks
