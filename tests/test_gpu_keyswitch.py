@@ -135,3 +135,23 @@ def test_keyswitch_rows_chunks(gpu):
     for b in (0, 63, 64, 66):
         np.testing.assert_array_equal(got[b], oracle.keyswitch(ct[b:b + 1], keys[b], q, dnum, 14, 3)[0],
                                       err_msg=f"ciphertext {b}")
+
+
+@pytest.mark.parametrize("L,dnum", [(3, 3), (4, 2), (5, 5), (2, 1)])
+def test_keyswitch_rows_shapes(gpu, L, dnum):
+    """Other (L, dnum) at N=16384 through the three-phase kernels (equal
+    digits of 1 or 2 primes, fewer float targets than one column thread
+    holds)."""
+    import torch
+    print(f"[ks] rows L={L} dnum={dnum}", flush=True)
+    n, batch = 16384, 5
+    q = cf.primes_below(50, 2 * n, L) + cf.primes_below(60, 2 * n, 1)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x50524147000A0000 + L).reshape(batch, 2, L, n)
+    keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x50524147000B0000 + dnum).reshape(
+        batch, dnum, 2, L + 1, n)
+    sw = praghip.Switch(q, 14, dnum, max_batch=batch)
+    tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
+    sw.keyswitch(tin, tout, keys=to_dev(keys), key_stride=sw.key_words, galois=2 * n - 1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(tout), oracle.keyswitch(ct, keys, q, dnum, 14, 2 * n - 1,
+                                                                    per_ct_keys=True))
