@@ -101,10 +101,13 @@ def bench_ntt(torch, praghip, steps, warmup):
     }
 
 
-def bench_keyswitch(torch, praghip, steps, warmup):
+def bench_keyswitch(torch, praghip, steps, warmup, reference=False):
+    """64 keyswitches with their own keys at N=16384, L=6: dnum=3 over six
+    ~50-bit data primes + a 60-bit special prime, or (reference=True) the
+    reference's own shape, dnum=6 over the seven locked 60-bit primes."""
     from praghip import params, synth
-    q = params.primes_n16384_switch()
-    L, dnum, batch = 6, 3, 64
+    q = list(params.LOCKED_PRIMES) if reference else params.primes_n16384_switch()
+    L, dnum, batch = 6, (6 if reference else 3), 64
     sw = praghip.Switch(q, LOG_N, dnum, max_batch=batch)
     ct = torch.empty(batch * 2 * L * N, dtype=torch.int64, device="cuda")
     out = torch.empty_like(ct)
@@ -126,7 +129,7 @@ def bench_keyswitch(torch, praghip, steps, warmup):
         "batch": batch, "dnum": dnum, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("keyswitch", 1),
+                     "traffic": None if reference else measured_traffic("keyswitch", 1),
                      "kernel": "whole keyswitch batch (all its launches); traffic is per batch",
                      "algorithmic_bytes_per_batch": batch * bytes_per_ks,
                      "algorithmic_bytes_per_keyswitch": bytes_per_ks},
@@ -461,6 +464,10 @@ def main() -> int:
         log("keyswitch N=16384 dnum=3, 64 ciphertexts ...")
         res["keyswitch"] = bench_keyswitch(torch, praghip, args.steps, args.warmup)
         log(f"keyswitch {res['keyswitch']['keyswitch_per_s']:.4g}/s")
+        log("keyswitch N=16384 dnum=6, locked 60-bit primes (the reference shape), 64 ciphertexts ...")
+        res["keyswitch_reference"] = bench_keyswitch(torch, praghip, args.steps, args.warmup, reference=True)
+        res["keyswitch_reference"].pop("_tensors")
+        log(f"keyswitch (reference shape) {res['keyswitch_reference']['keyswitch_per_s']:.4g}/s")
     if args.only in ("all", "gemm"):
         log("share GEMM 512x1024x3072 ...")
         res["gemm"] = bench_gemm(torch, praghip, args.steps, args.warmup)
