@@ -115,6 +115,11 @@ int praghip_switch_plan_create(int device, const uint64_t *q, size_t data_primes
  * [2][L][N] coefficient-form ciphertext -> Galois(element) + keyswitch -> host
  * [2][L][N]. */
 int praghip_switch_apply(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output);
+/* Switch::evaluate (switch.hpp:26, switch.cu:113-125): keyswitch only, host
+ * [2][L][N] coefficient-form ciphertext that the caller has already permuted
+ * by the plan's element (as keyswitch/seal_adapter.cpp:49-51 does on the CPU
+ * before calling evaluate) -> host [2][L][N].  No Galois gather. */
+int praghip_switch_evaluate(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output);
 /* Batched device keyswitch: in/out device [batch][2][L][N] (8-byte aligned);
  * keys device [dnum][2][L+1][N] per ciphertext at key_stride words apart (0:
  * one shared key; NULL keys: the plan's key), 16-byte aligned with an even

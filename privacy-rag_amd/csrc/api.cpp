@@ -665,15 +665,16 @@ int praghip_keyswitch(praghip_switch_plan* p, const uint64_t* input, uint64_t* o
   return PRAGHIP_OK;
 }
 
-int praghip_switch_apply(praghip_switch_plan* p, const uint64_t* input, uint64_t* output) {
+// Host round trip on the plan's stream: upload, keyswitch with Galois inverse
+// `ginv` (1: none), download, synchronous.
+static int switch_host_run(praghip_switch_plan* p, const uint64_t* input, uint64_t* output, uint32_t ginv,
+                           const char* what) {
   if (!p || !input || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (p->closing) return fail(PRAGHIP_E_CLOSED, "E_SWITCH_CLOSED");
   if (!p->key) return fail(PRAGHIP_E_STATE, "E_SWITCH_NO_KEY");
   const size_t n = size_t(1) << p->log_n, words = 2 * p->L * n;
   for (size_t i = 0; i < words; ++i)
     if (input[i] >= p->host_q[(i >> p->log_n) % p->L]) return fail(PRAGHIP_E_CANONICAL, "E_SWITCH_CIPHERTEXT");
-  uint32_t ginv = 1;
-  galois_inverse(p->element, p->log_n, ginv);
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
   hipStream_t s = p->stream;
@@ -691,12 +692,22 @@ int praghip_switch_apply(praghip_switch_plan* p, const uint64_t* input, uint64_t
   if (e == hipSuccess) e = hipEventElapsedTime(&t23, p->ev[2], p->ev[3]);
   if (e != hipSuccess) {
     std::memset(output, 0, words * 8);
-    return switch_failure(p, e, "apply");
+    return switch_failure(p, e, what);
   }
   p->timing.upload_ms = t01;
   p->timing.kernel_ms = t12;
   p->timing.download_ms = t23;
   return PRAGHIP_OK;
+}
+
+int praghip_switch_apply(praghip_switch_plan* p, const uint64_t* input, uint64_t* output) {
+  uint32_t ginv = 1;
+  if (p) galois_inverse(p->element, p->log_n, ginv);
+  return switch_host_run(p, input, output, ginv, "apply");
+}
+
+int praghip_switch_evaluate(praghip_switch_plan* p, const uint64_t* input, uint64_t* output) {
+  return switch_host_run(p, input, output, 1u, "evaluate");
 }
 
 int praghip_switch_sync(praghip_switch_plan* p) {

@@ -59,6 +59,7 @@ SIGNATURES = {
     "praghip_ntt_destroy": (None, [vp]),
     "praghip_switch_plan_create": (i32, [i32, vp, sz, u32, sz, vp, u32, sz, pp]),
     "praghip_switch_apply": (i32, [vp, vp, vp]),
+    "praghip_switch_evaluate": (i32, [vp, vp, vp]),
     "praghip_keyswitch": (i32, [vp, vp, vp, sz, vp, sz, u32, vp]),
     "praghip_switch_sync": (i32, [vp]),
     "praghip_switch_timing": (i32, [vp, ctypes.POINTER(Timing)]),

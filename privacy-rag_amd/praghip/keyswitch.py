@@ -46,6 +46,17 @@ class Switch:
         check(lib().praghip_switch_apply(self._h, host_ptr(src), host_ptr(out)))
         return out
 
+    def evaluate(self, ct) -> np.ndarray:
+        """Switch::evaluate (switch.cu:113-125): keyswitch only, on a host [2][L][N]
+        ciphertext already permuted by the plan's element (the reference's
+        apply permutes on the CPU first, keyswitch/seal_adapter.cpp:49-51)."""
+        src = host_u64(ct)
+        if src.size != (2 * self.L) << self.log_n:
+            raise shape_error("E_SWITCH_SHAPE")
+        out = np.empty_like(src)
+        check(lib().praghip_switch_evaluate(self._h, host_ptr(src), host_ptr(out)))
+        return out
+
     def keyswitch(self, ct, out, batch: int | None = None, keys=None, key_stride: int = 0, galois: int = 1,
                   stream=None):
         """Device [batch][2][L][N] -> [batch][2][L][N]; keys device tensor or None (plan key)."""

@@ -155,3 +155,63 @@ def test_keyswitch_rows_shapes(gpu, L, dnum):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(from_dev(tout), oracle.keyswitch(ct, keys, q, dnum, 14, 2 * n - 1,
                                                                     per_ct_keys=True))
+
+
+@pytest.mark.parametrize("log_n,element", [(14, 3), (14, (1 << 9) + 1), (12, 3), (12, (1 << 9) + 1)])
+def test_switch_evaluate_after_cpu_galois(gpu, log_n, element):
+    """The reference's calling convention (keyswitch/seal_adapter.cpp:44-52):
+    apply() permutes both components on the CPU, then Switch::evaluate
+    keyswitches.  The oracle's permutation fed through praghip_switch_evaluate
+    must equal the oracle's keyswitch with the element, and praghip_switch_apply
+    on the un-permuted input.  Elements 3 and 2^9 + 1 are packing levels 0 and
+    8 (bfv_acyclic_pack.hpp:44-52).  N = 16384 runs the three-phase kernels,
+    N = 4096 the fused one."""
+    q, L, dnum = cf.LOCKED_PRIMES, 6, 6
+    n = 1 << log_n
+    print(f"[ks] evaluate after CPU Galois log_n={log_n} element={element}", flush=True)
+    ct = oracle.fill_residues(2 * L, n, q[:L], 0x5052414700000C03 + log_n).reshape(2, L, n)
+    key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 0x5052414700010C03 + element).reshape(dnum, 2, L + 1, n)
+    permuted = np.stack([np.stack([oracle.galois(ct[c, i], q[i], log_n, element) for i in range(L)])
+                         for c in range(2)])
+    want = oracle.keyswitch(ct[None], key, q, dnum, log_n, element)[0]
+    sw = praghip.Switch(q, log_n, dnum, key=key, element=element)
+    np.testing.assert_array_equal(sw.evaluate(permuted), want)
+    np.testing.assert_array_equal(sw.apply(ct), want)
+    # element 1: evaluate and apply coincide
+    sw1 = praghip.Switch(q, log_n, dnum, key=key, element=1)
+    np.testing.assert_array_equal(sw1.evaluate(ct), sw1.apply(ct))
+
+
+@pytest.mark.parametrize("dnum", [2, 3])
+def test_keyswitch_locked_primes_multi_prime_digits(gpu, dnum):
+    """The seven locked 60-bit primes with digits of 3 or 2 primes: every
+    prime on the integer path, ModUp by fast base conversion in 64-bit
+    Shoup arithmetic (the column-forward kernel's ArU64 instance with D > 1)."""
+    q, n, L, batch = cf.LOCKED_PRIMES, 16384, 6, 2
+    print(f"[ks] locked primes dnum={dnum}", flush=True)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000D03 + dnum).reshape(batch, 2, L, n)
+    keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x5052414700010D03 + dnum).reshape(
+        batch, dnum, 2, L + 1, n)
+    want = oracle.keyswitch(ct, keys, q, dnum, 14, 5, per_ct_keys=True)
+    sw = praghip.Switch(q, 14, dnum, max_batch=batch)
+    tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
+    sw.keyswitch(tin, tout, keys=to_dev(keys), key_stride=sw.key_words, galois=5)
+    np.testing.assert_array_equal(from_dev(tout), want)
+
+
+def test_keyswitch_data_prime_below_2_32(gpu):
+    """A data prime below 2^32 keeps the data primes on the float path but
+    rules out the FP64 ModDown (it needs every data prime in (2^32, 2^50)):
+    the inverse columns then finish with the generic integer ModDown."""
+    n, L, dnum, batch = 16384, 6, 3, 2
+    q = cf.primes_below(31, n, 1) + cf.primes_below(50, n, L - 1) + cf.primes_below(60, n, 1)
+    assert q[0] < 1 << 32
+    print("[ks] data prime below 2^32", flush=True)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000E03).reshape(batch, 2, L, n)
+    keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x5052414700010E03).reshape(
+        batch, dnum, 2, L + 1, n)
+    want = oracle.keyswitch(ct, keys, q, dnum, 14, 3, per_ct_keys=True)
+    sw = praghip.Switch(q, 14, dnum, max_batch=batch)
+    tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
+    sw.keyswitch(tin, tout, keys=to_dev(keys), key_stride=sw.key_words, galois=3)
+    np.testing.assert_array_equal(from_dev(tout), want)
