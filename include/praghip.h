@@ -203,6 +203,19 @@ size_t praghip_local_dot_workspace_words(size_t slots);
 int praghip_local_dot_scale(int device, const uint64_t *shares, const uint64_t *weights, size_t words, size_t slots,
                             const uint64_t *delta, uint64_t r, const uint64_t *q, size_t primes, uint64_t *scaled,
                             uint64_t *workspace, void *stream);
+/* Allocation-free praghip_local_dot_scale.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  Same arguments and results without the
+ * workspace: the partial sums go to a static device array of
+ * PRAGHIP_NOALLOC_MAX_SLOTS x 256 words (128 KiB), one per device, held until
+ * the process ends.  slots above the limit: PRAGHIP_E_SHAPE
+ * (E_LOCAL_NOALLOC_SLOTS).  Every call on a device shares that array, so
+ * calls that overlap on one device (other streams, other threads) race; the
+ * caller serialises them.  Calls no allocating routine. */
+#define PRAGHIP_NOALLOC_MAX_SLOTS 64
+int praghip_local_dot_scale_noalloc(int device, const uint64_t *shares, const uint64_t *weights, size_t words,
+                                    size_t slots, const uint64_t *delta, uint64_t r, const uint64_t *q, size_t primes,
+                                    uint64_t *scaled, void *stream);
 
 /* ------------------------------------------------------- HE matrix product */
 /* matrix_gpu::Matrix (matrix.hpp:9-24, matrix.cu:48-81).  create: `input` is

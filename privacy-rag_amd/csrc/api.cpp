@@ -956,5 +956,27 @@ int praghip_local_dot_scale(int device, const uint64_t* shares, const uint64_t* 
   return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_LOCAL_HIP: ", e);
 }
 
+int praghip_local_dot_scale_noalloc(int device, const uint64_t* shares, const uint64_t* weights, size_t words,
+                                    size_t slots, const uint64_t* delta, uint64_t r, const uint64_t* q, size_t primes,
+                                    uint64_t* scaled, void* stream) {
+  if (slots == 0) return PRAGHIP_OK;
+  if (!shares || !weights || !delta || !scaled) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (slots > kNoAllocSlots) return fail(PRAGHIP_E_SHAPE, "E_LOCAL_NOALLOC_SLOTS: at most 64 slots");
+  if (!valid_moduli(q, primes) || words == 0 || r >= (1ull << 59)) return fail(PRAGHIP_E_SHAPE, "E_LOCAL_SHAPE");
+  for (size_t k = 0; k < primes; ++k)
+    if (delta[k] >= q[k]) return fail(PRAGHIP_E_CANONICAL, "E_LOCAL_DELTA");
+  if (!aligned8(shares) || !aligned8(weights) || !aligned8(scaled)) return fail(PRAGHIP_E_ARGUMENT, "E_LOCAL_ALIGNMENT");
+  Barrett m[kMaxKeyPrimes];
+  for (size_t i = 0; i < primes; ++i) m[i] = barrett_of(q[i]);
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  uint64_t* work = nullptr;
+  if (e == hipSuccess) e = local_dot_scratch(device, &work);
+  if (e == hipSuccess)
+    e = launch_local_dot_scale(shares, weights, words, slots, delta, r, m, int(primes), scaled, work,
+                               static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_LOCAL_HIP: ", e);
+}
+
 }  // extern "C"
 

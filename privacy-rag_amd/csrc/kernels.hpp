@@ -109,6 +109,11 @@ hipError_t launch_dyadic_mac(const uint64_t* a, const uint64_t* w, uint64_t* out
 hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,
                                   const uint64_t* delta, uint64_t r, const Barrett* m, int primes, uint64_t* scaled,
                                   uint64_t* work, hipStream_t s, size_t coords = 1);
+// Slot rows the allocation-free local dot takes: its scratch is
+// kNoAllocSlots * kLocalTiles words (128 KiB) per device.
+constexpr size_t kNoAllocSlots = 64;
+// Device address of that scratch on `device` (the current device).
+hipError_t local_dot_scratch(int device, uint64_t** address);
 
 // Token-resident path and packing tree (token.hip).
 hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint64_t* out, size_t slots,

@@ -10,6 +10,8 @@
 // chip.
 #include "kernels.hpp"
 
+#include <mutex>
+
 namespace praghip {
 
 static unsigned stream_grid(size_t items, unsigned per_block) {
@@ -241,6 +243,37 @@ hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weight
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(local_scale_kernel, dim3(rows), dim3(256), 0, s, work, tiles, sc, scaled);
   return hipGetLastError();
+}
+
+// ------------------------------------------- allocation-free local dot scratch
+// The per-tile partial sums of up to kNoAllocSlots slot rows of the local dot,
+// for callers that cannot allocate device memory.  Each device holds its own
+// copy until the process ends, and every call on a device shares it: calls that
+// overlap on one device race.  Every word a call reads was written by the same
+// call's first kernel, so nothing needs clearing.
+static __device__ __align__(256) uint64_t scratch[kNoAllocSlots * kLocalTiles];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mutex;
+uint64_t* scratch_address[kScratchDevices] = {};
+}  // namespace
+
+// Device address of `scratch` on `device`, which must be the current device.
+// Looked up once per device; the host-side name of the array is not a device
+// address and is never passed to a kernel or a copy.
+hipError_t local_dot_scratch(int device, uint64_t** address) {
+  if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_address[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    scratch_address[device] = static_cast<uint64_t*>(p);
+  }
+  *address = scratch_address[device];
+  return hipSuccess;
 }
 
 }  // namespace praghip

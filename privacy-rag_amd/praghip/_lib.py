@@ -74,6 +74,7 @@ SIGNATURES = {
     "praghip_dyadic_mac": (i32, [i32, vp, vp, vp, sz, sz, u32, sz, vp, sz, vp]),
     "praghip_local_dot_workspace_words": (sz, [sz]),
     "praghip_local_dot_scale": (i32, [i32, vp, vp, sz, sz, vp, u64, vp, sz, vp, vp, vp]),
+    "praghip_local_dot_scale_noalloc": (i32, [i32, vp, vp, sz, sz, vp, u64, vp, sz, vp, vp]),
     "praghip_matrix_plan_create": (i32, [i32, vp, sz, u32, vp, sz, pp]),
     "praghip_matrix_evaluate": (i32, [vp, vp, vp, vp, sz]),
     "praghip_matrix_evaluate_device": (i32, [vp, vp, vp, vp]),

@@ -169,6 +169,23 @@ def local_dot_scale(shares, weights, q, delta=None, r=None, out=None, stream=Non
     return out
 
 
+def local_dot_scale_noalloc(shares, weights, q, delta, r, out, stream=None):
+    """local_dot_scale through the allocation-free entry point: no workspace,
+    no allocation in the call (``out`` is required).  At most 64 slots; calls
+    that overlap on one device race on its static scratch."""
+    import numpy as np
+    slots, words = shares.shape
+    if weights.numel() != words or out.numel() < slots * len(q):
+        raise shape_error("E_LOCAL_SHAPE")
+    qa = np.ascontiguousarray(q, dtype=np.uint64)
+    da = np.ascontiguousarray(delta, dtype=np.uint64)
+    check(lib().praghip_local_dot_scale_noalloc(_dev(shares), dev_ptr(shares, u64_dtypes()),
+                                                dev_ptr(weights, u64_dtypes()), words, slots, da.ctypes.data, int(r),
+                                                qa.ctypes.data, len(qa), dev_ptr(out, u64_dtypes()),
+                                                stream_handle(stream)))
+    return out
+
+
 class LocalShares:
     """Host-vector mirror of prag::model::LocalShares (local_shares.hpp:22-32).
 

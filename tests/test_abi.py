@@ -121,6 +121,14 @@ def test_share_entry_points_validate_before_device():
     assert code(L.praghip_local_dot_scale(0, A, A, 16, 1, delta.ctypes.data, 1 << 59, q.ctypes.data, 2, A, A,
                                           None)) == (_lib.E_SHAPE, "E_LOCAL_SHAPE")
     assert L.praghip_local_dot_workspace_words(3) == 3 * 256
+    # the allocation-free variant: its scratch holds 64 slots; argument checks first
+    assert code(L.praghip_local_dot_scale_noalloc(0, A, A, 16, 65, delta.ctypes.data, 5, q.ctypes.data, 2, A,
+                                                  None)) == (_lib.E_SHAPE, "E_LOCAL_NOALLOC_SLOTS: at most 64 slots")
+    assert code(L.praghip_local_dot_scale_noalloc(0, A, None, 16, 1, delta.ctypes.data, 5, q.ctypes.data, 2, A,
+                                                  None)) == (_lib.E_ARGUMENT, "E_NULL")
+    assert code(L.praghip_local_dot_scale_noalloc(0, A, A, 16, 1, delta.ctypes.data, 5, q.ctypes.data, 2, A,
+                                                  None)) == (_lib.E_CANONICAL, "E_LOCAL_DELTA")
+    assert L.praghip_local_dot_scale_noalloc(0, None, None, 16, 0, None, 5, None, 0, None, None) == _lib.OK
     descs = (_lib.GemmDesc * 2)(_lib.GemmDesc(A, A, None, A, 4, 8, 4, 8, 64), _lib.GemmDesc(A, A, None, A, 4, 8, 4, 16, 64))
     assert code(L.praghip_share_gemm_batch(0, ctypes.cast(descs, ctypes.c_void_p), 2, None)) == (
         _lib.E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE")
