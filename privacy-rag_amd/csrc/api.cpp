@@ -538,6 +538,7 @@ int build_ks_const(const uint64_t* q, size_t L, size_t dnum, unsigned log_n, KsC
     kc.q[t] = q[t];
     const u128 ratio = (~(u128)0) / q[t];
     kc.bar[t] = Barrett{q[t], uint64_t(ratio), uint64_t(ratio >> 64)};
+    kc.one_q[t] = shoup_q(1, q[t]);
   }
   for (size_t i = 0; i < L; ++i) {
     const int j = kc.digit_of[i];
@@ -556,7 +557,6 @@ int build_ks_const(const uint64_t* q, size_t L, size_t dnum, unsigned log_n, KsC
     const uint64_t ip = invmod(p % q[i], q[i]);
     kc.invp[i] = Shoup{ip, shoup_q(ip, q[i])};
     kc.half_mod[i] = (p >> 1) % q[i];
-    kc.one_q[i] = shoup_q(1, q[i]);
   }
   return PRAGHIP_OK;
 }

@@ -42,7 +42,7 @@ struct KsConst {
   Shoup hat[kMaxKeyPrimes][kMaxKeyPrimes];  // (Q_j/q_i) mod q_t, mod q_t   [i][t]
   Shoup invp[kMaxKeyPrimes];             // p^-1 mod q_i
   uint64_t half_mod[kMaxKeyPrimes];      // floor(p/2) mod q_i
-  uint64_t one_q[kMaxKeyPrimes];         // floor(2^64 / q_i): Shoup constant of 1
+  uint64_t one_q[kMaxKeyPrimes];         // floor(2^64 / q_t): Shoup constant of 1, every key prime
 };
 
 struct KsArgs {

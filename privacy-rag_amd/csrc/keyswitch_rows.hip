@@ -52,6 +52,7 @@ struct KsRows {
   uint32_t ginv;
   int data_f64;     // every data prime below 2^50: data primes take the float path
   int moddown_f64;  // every data prime in (2^32, 2^50): ModDown in FP64 too
+  int narrow;       // every key prime below twice every other: x mod q_t by one subtraction
   unsigned b0, cts;  // chunk: ciphertexts b0 .. b0 + cts - 1
 };
 
@@ -182,6 +183,16 @@ constexpr unsigned kColTargets() {
   return std::is_same<typename A::T, double>::value ? 6u : 1u;
 }
 
+// x mod q_t for a canonical residue x of another key prime: one conditional
+// subtraction when every key prime is below twice every other (`narrow`; the
+// reference's decomposition at switch.cu:63-68 and its ModDown at :74-82 rely
+// on it for the locked primes), a Shoup product by 1 otherwise.
+__device__ __forceinline__ uint64_t reduce_to(uint64_t x, const KsConst& kc, int t, int narrow) {
+  const uint64_t qt = kc.q[t];
+  if (narrow) return x >= qt ? x - qt : x;
+  return mul_shoup(x, 1, kc.one_q[t], qt);
+}
+
 // One thread per (ciphertext, digit, group of up to G targets, column), for
 // the targets t_lo .. t_lo + t_n - 1 of one arithmetic policy (A = ArF64Lean:
 // float-path data primes; ArU64: the integer-path primes); digits of exactly
@@ -200,12 +211,27 @@ __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, un
   const uint64_t* c1 = f.in + ((size_t(b) * 2 + 1) * L << kLog);
   uint64_t y[D][kE];
   const unsigned t_first = t_lo + g * G, t_end = t_lo + (g * G + G < t_n ? g * G + G : t_n);
-  if (G > 1) digit_factors<D, A>(y, f, kc, c1, lo, c);
+  if constexpr (D == 1) {
+    // one prime per digit: (Q_j / q_i) = 1, so the digit expands to its own
+    // canonical residues, reduced mod each target below
+#pragma unroll
+    for (int k = 0; k < kE; ++k) y[0][k] = gather(c1 + (size_t(lo) << kLog), c + (unsigned(k) << kRowLog), f.ginv, kc.q[lo]);
+  } else if (G > 1) {
+    digit_factors<D, A>(y, f, kc, c1, lo, c);
+  }
   for (unsigned t = t_first; t < t_end; ++t) {
     const NttPrime pt = f.primes[t];
     const A ar(pt);
     T v[kE];
-    if (int(t) >= lo && int(t) < lo + D) {  // a prime of the digit: its own residues
+    if constexpr (D == 1) {
+      if (int(t) == lo) {
+#pragma unroll
+        for (int k = 0; k < kE; ++k) v[k] = ar.from_u64(y[0][k]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kE; ++k) v[k] = ar.from_u64(reduce_to(y[0][k], kc, int(t), f.narrow));
+      }
+    } else if (int(t) >= lo && int(t) < lo + D) {  // a prime of the digit: its own residues
 #pragma unroll
       for (int k = 0; k < kE; ++k)
         v[k] = ar.from_u64(gather(c1 + (size_t(t) << kLog), c + (unsigned(k) << kRowLog), f.ginv, pt.q));
@@ -564,7 +590,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWa
 #pragma unroll
   for (int k = 0; k < kE; ++k) {
     const uint64_t last = pc[(size_t(L) << kLog) + (unsigned(k) << kRowLog)];
-    const uint64_t reduced = mul_shoup(last, 1, kc.one_q[i], qi);  // last mod q_i
+    const uint64_t reduced = reduce_to(last, kc, int(i), f.narrow);  // last mod q_i
     const uint64_t corr = sub_mod(reduced, kc.half_mod[i], qi);
     uint64_t val = mul_shoup(sub_mod(x[k], corr, qi), kc.invp[i].w, kc.invp[i].wq, qi);
     if (comp == 0) val = add_mod(val, gather(c0, c + (unsigned(k) << kRowLog), f.ginv, qi), qi);
@@ -624,6 +650,12 @@ hipError_t launch_keyswitch_rows(const KsArgs& a, const KsConst* kc_dev, const K
     f.data_f64 &= kc.q[i] < (1ull << 50) ? 1 : 0;
     f.moddown_f64 &= (kc.q[i] < (1ull << 50) && kc.q[i] > (1ull << 32)) ? 1 : 0;
   }
+  uint64_t q_max = 0, q_min = ~0ull;
+  for (int t = 0; t < kc.K; ++t) {
+    q_max = std::max(q_max, kc.q[t]);
+    q_min = std::min(q_min, kc.q[t]);
+  }
+  f.narrow = q_max / 2 < q_min ? 1 : 0;  // q_max < 2 q_min
   const unsigned K = unsigned(kc.K), L = unsigned(kc.L), dnum = unsigned(kc.dnum), rows = kN >> kRowLog;
   for (size_t b0 = 0; b0 < a.batch; b0 += a.inter_cts) {
     f.b0 = unsigned(b0);

@@ -10,44 +10,77 @@
 
 namespace praghip {
 
-// Transform of one limb: coalesced loads in the first pass's layout, the
-// passes in registers + LDS, stores in the last pass's layout.
-template <int LOGN, bool INV, class A>
-__device__ __forceinline__ void transform_limb(uint64_t* __restrict__ x, const typename A::TW* __restrict__ tab,
-                                               const NttPrime& pr, uint64_t* lds) {
-  using T = typename A::T;
-  const unsigned t = threadIdx.x;
-  const A ar(pr);
-  T v[kE];
-#pragma unroll
-  for (int j = 0; j < kE; ++j)
-    v[j] = ar.from_u64(x[INV ? inv_in_index<LOGN>(t, j) : fwd_in_index<LOGN>(t, j)]);
-  ntt_regs<LOGN, INV>(v, reinterpret_cast<T*>(lds), t, tab, ar, pr, [&] {});
-  if (!INV) {
-#pragma unroll
-    for (int j = 0; j < kE; j += 2)
-      *reinterpret_cast<ulonglong2*>(x + fwd_out_index<LOGN>(t, j)) =
-          make_ulonglong2(ar.to_u64_fwd(v[j]), ar.to_u64_fwd(v[j + 1]));
-  } else {
-#pragma unroll
-    for (int j = 0; j < kE; ++j) x[inv_out_index<LOGN>(t, j)] = ar.to_u64_inv(v[j]);
-  }
-}
-
 // Kernel over the limbs whose prime uses arithmetic A: virtual index v maps to
 // limb (v / C) * P + sel[v % C], where sel lists the C prime indices of that
 // arithmetic.  Workgroup g transforms v = g, g + G, ... (G resident
-// workgroups).
+// workgroups).  Each limb is loaded in the first pass's layout (coalesced),
+// transformed in registers + LDS and stored in the last pass's layout.  The
+// float-path forward kernel issues the next limb's loads as soon as the
+// current limb no longer needs the LDS (before its last pass), so they overlap
+// the last pass and the stores instead of starting after them; the other
+// kernels have no registers to spare for them and load each limb at the top
+// of its turn.
 template <int LOGN, bool INV, class A>
 __global__ void __launch_bounds__(ntt_threads<LOGN>())
     ntt_kernel(uint64_t* __restrict__ data, size_t count, const NttPrime* __restrict__ primes,
                const typename A::TW* __restrict__ tw, int P, const int* __restrict__ sel, int C) {
   __shared__ __attribute__((aligned(16))) uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
-  for (size_t v = blockIdx.x; v < count; v += gridDim.x) {
-    const size_t limb = (v / unsigned(C)) * unsigned(P) + unsigned(sel[v % unsigned(C)]);
-    const int p = int(limb % unsigned(P));
-    const NttPrime pr = primes[p];
-    transform_limb<LOGN, INV, A>(data + (limb << LOGN), tw + (size_t(p) << LOGN), pr, lds);
+  using T = typename A::T;
+  const unsigned t = threadIdx.x;
+  const auto limb_of = [&](size_t v) { return (v / unsigned(C)) * unsigned(P) + unsigned(sel[v % unsigned(C)]); };
+  const auto in_index = [&](int j) { return INV ? inv_in_index<LOGN>(t, j) : fwd_in_index<LOGN>(t, j); };
+  const auto store = [&](const A& ar, T (&x)[kE], size_t limb) {
+    uint64_t* out = data + (limb << LOGN);
+    if (!INV) {
+#pragma unroll
+      for (int j = 0; j < kE; j += 2)
+        *reinterpret_cast<ulonglong2*>(out + fwd_out_index<LOGN>(t, j)) =
+            make_ulonglong2(ar.to_u64_fwd(x[j]), ar.to_u64_fwd(x[j + 1]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < kE; ++j) out[inv_out_index<LOGN>(t, j)] = ar.to_u64_inv(x[j]);
+    }
+  };
+  if constexpr (std::is_same<T, double>::value && !INV) {
+    size_t v = blockIdx.x;
+    if (v >= count) return;
+    uint64_t raw[kE];
+    {
+      const uint64_t* x = data + (limb_of(v) << LOGN);
+#pragma unroll
+      for (int j = 0; j < kE; ++j) raw[j] = x[in_index(j)];
+    }
+    for (; v < count; v += gridDim.x) {
+      const size_t limb = limb_of(v);
+      const int p = int(limb % unsigned(P));
+      const NttPrime pr = primes[p];
+      const A ar(pr);
+      T x[kE];
+#pragma unroll
+      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(raw[j]);
+      const size_t vn = v + gridDim.x;
+      ntt_regs<LOGN, INV>(x, reinterpret_cast<T*>(lds), t, tw + (size_t(p) << LOGN), ar, pr, [&] {
+        if (vn < count) {
+          const uint64_t* xn = data + (limb_of(vn) << LOGN);
+#pragma unroll
+          for (int j = 0; j < kE; ++j) raw[j] = xn[in_index(j)];
+        }
+      });
+      store(ar, x, limb);
+    }
+  } else {
+    for (size_t v = blockIdx.x; v < count; v += gridDim.x) {
+      const size_t limb = limb_of(v);
+      const int p = int(limb % unsigned(P));
+      const NttPrime pr = primes[p];
+      const A ar(pr);
+      const uint64_t* xv = data + (limb << LOGN);
+      T x[kE];
+#pragma unroll
+      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(xv[in_index(j)]);
+      ntt_regs<LOGN, INV>(x, reinterpret_cast<T*>(lds), t, tw + (size_t(p) << LOGN), ar, pr);
+      store(ar, x, limb);
+    }
   }
 }
 
