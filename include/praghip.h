@@ -176,6 +176,25 @@ int praghip_ring_layout(int device, const uint64_t *a, size_t n_in, const uint64
 int praghip_ring_sum_rows(int device, const uint64_t *a, uint64_t *out, size_t rows, size_t cols, int mask_bits,
                           void *stream);
 
+/* ShareStorage of LocalShares::allocate (local_shares.hpp:12-17,29,
+ * local_shares.cu:14-24): `words` device words of one participant's ring-2^59
+ * shares, zero-filled on allocation (E_CUDA_SHAPE for 0 words).  write: host
+ * words[count] -> storage[offset..], each < 2^59 (E_CUDA_WORD), inside the
+ * storage (E_CUDA_SHAPE); read: storage[offset..offset+count) -> host; both
+ * synchronous on the storage's own stream.  data: the device address (for the
+ * ring ops and the share GEMM).  clear (ShareStorage::clear): wipes with
+ * zeros, synchronises and frees, idempotent, reported like a plan's close;
+ * later calls return E_CUDA_STORAGE_CLOSED.  stats: bytes uploaded and
+ * downloaded (LocalShareStats, local_shares.hpp:18-21). */
+typedef struct praghip_share_storage praghip_share_storage;
+int praghip_storage_allocate(int device, size_t words, praghip_share_storage **storage);
+int praghip_storage_write(praghip_share_storage *storage, size_t offset, const uint64_t *words, size_t count);
+int praghip_storage_read(praghip_share_storage *storage, size_t offset, size_t count, uint64_t *out);
+int praghip_storage_data(praghip_share_storage *storage, uint64_t **data, size_t *words);
+int praghip_storage_stats(const praghip_share_storage *storage, uint64_t *uploaded_bytes, uint64_t *downloaded_bytes);
+int praghip_storage_clear(praghip_share_storage *storage, praghip_cleanup *out);
+void praghip_storage_destroy(praghip_share_storage *storage);
+
 /* Centred lift of ring-2^59 words into RNS residues (matrix.cu:23-26 lift for
  * width 0; resident.cu:23-30 lift for width > 0): out[b][k][z] = the signed
  * value of v (v - 2^59 when bit 58 is set) mod q_k, canonical; for q_k > 2^59
@@ -245,9 +264,35 @@ int praghip_matrix_evaluate_device(praghip_matrix_plan *plan, const uint64_t *ri
 int praghip_matrix_reserve(praghip_matrix_plan *plan, size_t groups);
 int praghip_matrix_evaluate_device_batch(praghip_matrix_plan *plan, const uint64_t *rings, uint64_t *output,
                                          size_t groups, void *stream);
+/* evaluate_selective for a batch, on the device (matrix.cu:65-81 with the
+ * gather_c0 kernel of matrix.cu:41-44): as evaluate_device_batch, then c0 of
+ * every group keeps only the `count` target coefficients `targets` (host,
+ * 1..512 strictly increasing indices < 2^log_n; MATRIX_GPU_TARGET_COUNT,
+ * MATRIX_GPU_TARGET_INDEX) and is zero elsewhere; c1 is complete.  selected
+ * (device [groups][primes][count], 16-byte aligned, or NULL) receives the
+ * gathered target coefficients of c0. */
+int praghip_matrix_evaluate_device_batch_selective(praghip_matrix_plan *plan, const uint64_t *rings,
+                                                   uint64_t *output, size_t groups, const uint64_t *targets,
+                                                   size_t count, uint64_t *selected, void *stream);
 size_t praghip_matrix_device_bytes(const praghip_matrix_plan *plan);
 int praghip_matrix_close(praghip_matrix_plan *plan, praghip_cleanup *out);
 void praghip_matrix_destroy(praghip_matrix_plan *plan);
+
+/* Packing of a matrix product (prag::MatrixPacking, matrix_packing and
+ * matrix_packing_qk_reverse64 at native/include/prag/bfv_layout.hpp:8-27,
+ * called from bfv_matrix.inc:9 and bfv.cpp:689): for `batch` rows, `inner`
+ * terms and `outputs` columns, the reduction width, output columns per
+ * returned ciphertext, returned ciphertexts and input ciphertexts of the
+ * cheapest packing (bytes = inputs x 1,572,960 + returns x 786,528; ties take
+ * the smallest width).  E_MATRIX_SHAPE unless 1 <= batch <= 16,
+ * 1 <= inner <= 8192, 1 <= outputs <= 155,648; qk_reverse64 != 0 is the
+ * dedicated K = 128, one-output layout {128, 1, 1, 1} (E_QK_REVERSE64_SHAPE
+ * unless 1 <= batch <= 64).  Host only. */
+typedef struct praghip_matrix_packing_t {
+  uint64_t reduction, columns, returns, inputs;
+} praghip_matrix_packing_t;
+int praghip_matrix_packing(size_t batch, size_t inner, size_t outputs, int qk_reverse64,
+                           praghip_matrix_packing_t *out);
 
 /* ------------------------------------------- public-key encryption of zero */
 /* prag::enc0_gpu::PublicZero (enc0.hpp:15-25, enc0.cu:99-114): create takes
@@ -336,6 +381,14 @@ int praghip_token_stack_store(praghip_token_plan *plan, size_t slot, unsigned le
                               void *stream);
 int praghip_token_stack_view(praghip_token_plan *plan, size_t slot, unsigned level, const uint64_t **view);
 int praghip_token_download(praghip_token_plan *plan, const uint64_t *view, uint64_t *output);
+/* stack_store and download with the view's ready event, as the reference's
+ * DeviceCipherBatch carries one (resident.hpp:17-20; resident.cu:176-179,
+ * 187-189): `ready` is a hipEvent_t recorded after the producer's writes
+ * (required: E_DEVICE_STACK_VIEW / E_DEVICE_DOWNLOAD_VIEW when NULL); the
+ * plan's own stream waits on it, copies, and the call waits for the copy. */
+int praghip_token_stack_store_ready(praghip_token_plan *plan, size_t slot, unsigned level, const uint64_t *view,
+                                    void *ready);
+int praghip_token_download_ready(praghip_token_plan *plan, const uint64_t *view, void *ready, uint64_t *output);
 int praghip_token_timing(const praghip_token_plan *plan, praghip_timing *out);
 int praghip_token_close(praghip_token_plan *plan, praghip_cleanup *out);
 void praghip_token_destroy(praghip_token_plan *plan);
@@ -369,6 +422,12 @@ int praghip_pack_pair_device(praghip_pack_plan *plan, const uint64_t *left, cons
                              unsigned level, uint64_t *output, void *stream);
 int praghip_pack_tree_device(praghip_pack_plan *plan, uint64_t *nodes, size_t leaves, size_t slots, void *stream);
 int praghip_pack_merges(const praghip_pack_plan *plan, uint64_t *merges);
+/* packed_target (bfv_acyclic_pack.hpp:53-56): the coefficient on which
+ * coordinate `coordinate` (its low `levels` bits) lands after a packing tree of
+ * `levels` levels at N = 2^log_n: those bits reversed, times N >> levels (the
+ * reference: levels 9, log_n 14, spacing 32).  E_PACK_KEY_LEVELS unless
+ * 1 <= levels <= log_n <= 14.  Host only. */
+int praghip_packed_target(size_t coordinate, unsigned levels, uint32_t log_n, uint64_t *target);
 int praghip_pack_timing(const praghip_pack_plan *plan, praghip_timing *out);
 int praghip_pack_close(praghip_pack_plan *plan, praghip_cleanup *out);
 void praghip_pack_destroy(praghip_pack_plan *plan);

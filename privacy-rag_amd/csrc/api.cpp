@@ -600,12 +600,15 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
   if (e == hipSuccess) e = hipMemcpyAsync(p->kc_dev, &p->kc, sizeof(KsConst), hipMemcpyHostToDevice, p->stream);
   if (e == hipSuccess && key) e = p->buf.alloc((void**)&p->key, key_words * 8, true);
   if (e == hipSuccess && key) e = hipMemcpyAsync(p->key, key, key_words * 8, hipMemcpyHostToDevice, p->stream);
-  if (e == hipSuccess) {
+  // the fused kernel's running sums and work queue, only for shapes the
+  // three-phase kernels do not take (they never touch either)
+  const bool fused = !keyswitch_rows_supported(p->kc);
+  if (e == hipSuccess && fused) {
     p->acc_slots = ks_acc_slots(int(log_n));
     e = p->acc_slots ? p->buf.alloc((void**)&p->acc, size_t(p->acc_slots) * 2 * n * 8, true) : hipErrorInvalidValue;
   }
-  if (e == hipSuccess) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
-  if (e == hipSuccess) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
+  if (e == hipSuccess && fused) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
+  if (e == hipSuccess && fused) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, max_batch * 2 * K * n * 8, true);
   if (e == hipSuccess && keyswitch_rows_supported(p->kc)) {
     p->inter_cts = std::min(max_batch, kKsRowsChunk);
@@ -955,6 +958,115 @@ int praghip_local_dot_scale(int device, const uint64_t* shares, const uint64_t* 
                                static_cast<hipStream_t>(stream));
   return e == hipSuccess ? PRAGHIP_OK : hip_fail("E_LOCAL_HIP: ", e);
 }
+
+// ============================================================ ShareStorage
+// prag::model::ShareStorage from LocalShares::allocate (local_shares.hpp:12-17,
+// 29; local_shares.cu:14-24): device words of one participant's shares,
+// zero-filled on allocation; write/read are synchronous host copies on the
+// storage's own stream; clear wipes, synchronises and frees.
+}  // extern "C"
+
+struct praghip_share_storage {
+  int device = -1;
+  size_t words = 0;
+  Buffers buf;
+  uint64_t* data = nullptr;
+  hipStream_t stream = nullptr;
+  praghip_cleanup cleanup{};
+  uint64_t uploaded = 0, downloaded = 0;
+  bool closing = false;
+  void release() { release_all(device, buf, stream, nullptr, 0, cleanup, closing); }
+  ~praghip_share_storage() { release(); }
+};
+
+namespace {
+int storage_failure(praghip_share_storage* st, hipError_t e, const char* what) {
+  st->release();
+  return fail(PRAGHIP_E_DEVICE, std::string("E_CUDA_LOCAL: ") + what + ": " + hipGetErrorString(e));
+}
+int storage_range(const praghip_share_storage* st, size_t offset, size_t count) {
+  if (!st) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (st->closing) return fail(PRAGHIP_E_CLOSED, "E_CUDA_STORAGE_CLOSED");
+  if (offset > st->words || count > st->words - offset) return fail(PRAGHIP_E_SHAPE, "E_CUDA_SHAPE");
+  return PRAGHIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int praghip_storage_allocate(int device, size_t words, praghip_share_storage** out) {
+  if (!out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *out = nullptr;
+  if (words == 0 || words > SIZE_MAX / 8) return fail(PRAGHIP_E_SHAPE, "E_CUDA_SHAPE");
+  if (int rc = check_device(device)) return rc;
+  std::unique_ptr<praghip_share_storage> st(new praghip_share_storage);
+  st->device = device;
+  st->words = words;
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = st->buf.alloc((void**)&st->data, words * 8, true);
+  if (e == hipSuccess) e = hipMemsetAsync(st->data, 0, words * 8, st->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+  if (e != hipSuccess) return storage_failure(st.get(), e, "allocate");
+  *out = st.release();
+  return PRAGHIP_OK;
+}
+
+int praghip_storage_write(praghip_share_storage* st, size_t offset, const uint64_t* words, size_t count) {
+  if (int rc = storage_range(st, offset, count)) return rc;
+  if (count && !words) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  for (size_t i = 0; i < count; ++i)
+    if (words[i] >> 59) return fail(PRAGHIP_E_CANONICAL, "E_CUDA_WORD");
+  if (!count) return PRAGHIP_OK;
+  DeviceScope scope(st->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipMemcpyAsync(st->data + offset, words, count * 8, hipMemcpyHostToDevice, st->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+  if (e != hipSuccess) return storage_failure(st, e, "write");
+  st->uploaded += count * 8;
+  return PRAGHIP_OK;
+}
+
+int praghip_storage_read(praghip_share_storage* st, size_t offset, size_t count, uint64_t* out) {
+  if (int rc = storage_range(st, offset, count)) return rc;
+  if (count && !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (!count) return PRAGHIP_OK;
+  DeviceScope scope(st->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipMemcpyAsync(out, st->data + offset, count * 8, hipMemcpyDeviceToHost, st->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+  if (e != hipSuccess) {
+    std::memset(out, 0, count * 8);
+    return storage_failure(st, e, "read");
+  }
+  st->downloaded += count * 8;
+  return PRAGHIP_OK;
+}
+
+int praghip_storage_data(praghip_share_storage* st, uint64_t** data, size_t* words) {
+  if (!st || !data) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (st->closing) return fail(PRAGHIP_E_CLOSED, "E_CUDA_STORAGE_CLOSED");
+  *data = st->data;
+  if (words) *words = st->words;
+  return PRAGHIP_OK;
+}
+
+int praghip_storage_stats(const praghip_share_storage* st, uint64_t* uploaded_bytes, uint64_t* downloaded_bytes) {
+  if (!st) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (uploaded_bytes) *uploaded_bytes = st->uploaded;
+  if (downloaded_bytes) *downloaded_bytes = st->downloaded;
+  return PRAGHIP_OK;
+}
+
+int praghip_storage_clear(praghip_share_storage* st, praghip_cleanup* out) {
+  if (!st) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  st->release();
+  if (out) *out = st->cleanup;
+  return PRAGHIP_OK;
+}
+
+void praghip_storage_destroy(praghip_share_storage* st) { delete st; }
 
 int praghip_local_dot_scale_noalloc(int device, const uint64_t* shares, const uint64_t* weights, size_t words,
                                     size_t slots, const uint64_t* delta, uint64_t r, const uint64_t* q, size_t primes,

@@ -126,6 +126,12 @@ hipError_t launch_token_mac(const uint64_t* in, const uint64_t* w, uint64_t* out
 hipError_t launch_pack_prepare(const uint64_t* left, const uint64_t* right, uint64_t* sum, uint64_t* diff,
                                size_t count, size_t first, size_t group, size_t stride, const PrimeList& pl,
                                int log_n, size_t shift, uint32_t ginv, hipStream_t s);
+// Selective batch output: c0 of each group [groups][2][primes][2^log_n] zero
+// outside the `count` (<= kMaxTargets) sorted target coefficients idx[], and
+// the targets gathered into selected [groups][primes][count] (if non-null).
+constexpr unsigned kMaxTargets = 512;
+hipError_t launch_select_c0(uint64_t* out, size_t groups, int primes, int log_n, const uint64_t* idx,
+                            unsigned count, uint64_t* selected, hipStream_t s);
 hipError_t launch_pack_finish(const uint64_t* a, const uint64_t* b, uint64_t* out, size_t count, const PrimeList& pl,
                               int log_n, hipStream_t s);
 

@@ -29,6 +29,7 @@ struct praghip_matrix_plan {
   uint64_t *input = nullptr, *ring = nullptr, *weight = nullptr, *output = nullptr;
   size_t batch_cap = 0;
   uint64_t* bweight = nullptr;  // [batch_cap][blocks][P][N] transformed weight limbs
+  uint64_t* indices = nullptr;  // [512] target coefficients of a selective batch
   hipStream_t stream = nullptr;
   hipEvent_t ev[1] = {};
   praghip_cleanup cleanup{};
@@ -87,6 +88,7 @@ int praghip_matrix_plan_create(int device, const uint64_t* q, size_t primes, uin
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->ring, blocks * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->weight, blocks * primes * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->output, 2 * primes * n * 8, true);
+  if (e == hipSuccess) e = p->buf.alloc((void**)&p->indices, kMaxTargets * 8, false);
   if (e == hipSuccess) e = hipMemcpyAsync(p->input, input, in_words * 8, hipMemcpyHostToDevice, p->stream);
   if (e == hipSuccess) e = launch_ntt(false, p->input, blocks * 2 * primes, p->d, p->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
@@ -154,17 +156,34 @@ int praghip_matrix_reserve(praghip_matrix_plan* p, size_t groups) {
   return PRAGHIP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// Target list of evaluate_selective (matrix.cu:65-68): 1..512 strictly
+// increasing coefficient indices below N.
+int check_targets(const uint64_t* targets, size_t count, size_t n) {
+  if (count == 0 || count > kMaxTargets) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_TARGET_COUNT");
+  for (size_t i = 0; i < count; ++i)
+    if (targets[i] >= n || (i && targets[i] <= targets[i - 1])) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_TARGET_INDEX");
+  return PRAGHIP_OK;
+}
+}  // namespace
+
 // Many output groups per call: lift and transform every group's weight limbs,
 // one column-batched sum of products over the resident blocks, one inverse
-// transform over all outputs.
-int praghip_matrix_evaluate_device_batch(praghip_matrix_plan* p, const uint64_t* rings, uint64_t* output,
-                                         size_t groups, void* stream) {
+// transform over all outputs.  With targets: the device-side selective form
+// (c0 kept at the targets only, gathered into `selected`).
+static int matrix_batch(praghip_matrix_plan* p, const uint64_t* rings, uint64_t* output, size_t groups,
+                        const uint64_t* targets, size_t count, uint64_t* selected, void* stream) {
   if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (p->closing) return fail(PRAGHIP_E_CLOSED, "MATRIX_GPU_CLOSED");
+  if (targets)
+    if (int rc = check_targets(targets, count, size_t(1) << p->log_n)) return rc;
   if (groups == 0) return PRAGHIP_OK;
   if (!rings || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (groups > p->batch_cap) return fail(PRAGHIP_E_SHAPE, "MATRIX_GPU_BATCH");
-  if ((reinterpret_cast<uintptr_t>(rings) | reinterpret_cast<uintptr_t>(output)) & 15)
+  if ((reinterpret_cast<uintptr_t>(rings) | reinterpret_cast<uintptr_t>(output) |
+       reinterpret_cast<uintptr_t>(selected)) & 15)
     return fail(PRAGHIP_E_ARGUMENT, "MATRIX_GPU_ALIGNMENT");
   PrimeList pl{};
   for (size_t i = 0; i < p->P; ++i) pl.q[i] = p->host_q[i];
@@ -179,7 +198,58 @@ int praghip_matrix_evaluate_device_batch(praghip_matrix_plan* p, const uint64_t*
   if (e == hipSuccess)
     e = launch_token_mac(p->input, p->bweight, output, groups, p->blocks, 2 * p->P, int(p->log_n), m, int(p->P), s);
   if (e == hipSuccess) e = launch_ntt(true, output, groups * 2 * p->P, p->d, s);
+  if (e == hipSuccess && targets) e = hipMemcpyAsync(p->indices, targets, count * 8, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && targets)
+    e = launch_select_c0(output, groups, int(p->P), int(p->log_n), p->indices, unsigned(count), selected, s);
   if (e != hipSuccess) return matrix_failure(p, e, "evaluate_device_batch");
+  return PRAGHIP_OK;
+}
+
+extern "C" {
+
+int praghip_matrix_evaluate_device_batch(praghip_matrix_plan* p, const uint64_t* rings, uint64_t* output,
+                                         size_t groups, void* stream) {
+  return matrix_batch(p, rings, output, groups, nullptr, 0, nullptr, stream);
+}
+
+int praghip_matrix_evaluate_device_batch_selective(praghip_matrix_plan* p, const uint64_t* rings, uint64_t* output,
+                                                   size_t groups, const uint64_t* targets, size_t count,
+                                                   uint64_t* selected, void* stream) {
+  if (!targets) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  return matrix_batch(p, rings, output, groups, targets, count, selected, stream);
+}
+
+// The cost model that sizes a packed matrix product (bfv_layout.hpp:8-27):
+// for a batch of b rows, inner dimension k and o outputs, every power-of-two
+// reduction width d in [16, 8192/b] packs up to cap = min(512/b, 8192/(b d))
+// output columns per returned ciphertext; the choice minimises the bytes moved,
+// ceil(k/d) input ciphertexts of 1,572,960 B plus the returned ciphertexts of
+// 786,528 B, the first (smallest) d winning ties.  qk_reverse64 is the
+// dedicated single-output product of 128 terms, for b <= 64.
+int praghip_matrix_packing(size_t batch, size_t inner, size_t outputs, int qk_reverse64, praghip_matrix_packing_t* out) {
+  if (!out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *out = praghip_matrix_packing_t{0, 0, 0, 0};
+  if (qk_reverse64) {
+    if (batch == 0 || batch > 64) return fail(PRAGHIP_E_SHAPE, "E_QK_REVERSE64_SHAPE");
+    *out = praghip_matrix_packing_t{128, 1, 1, 1};
+    return PRAGHIP_OK;
+  }
+  if (batch == 0 || batch > 16 || inner == 0 || inner > 8192 || outputs == 0 || outputs > 155648)
+    return fail(PRAGHIP_E_SHAPE, "E_MATRIX_SHAPE");
+  const uint64_t kInputBytes = 1572960, kReturnBytes = 786528;
+  const size_t per_group = 512 / batch;  // output columns one packed group holds
+  const size_t whole = outputs / per_group, rest = outputs % per_group;
+  uint64_t best = ~uint64_t(0);
+  for (size_t width = 16; width <= 8192 / batch; width <<= 1) {
+    const size_t cap = std::min(per_group, 8192 / (batch * width));
+    const size_t returns = whole * ((per_group + cap - 1) / cap) + (rest ? (rest + cap - 1) / cap : 0);
+    const size_t inputs = (inner + width - 1) / width;
+    const uint64_t bytes = inputs * kInputBytes + returns * kReturnBytes;
+    if (bytes < best) {
+      best = bytes;
+      *out = praghip_matrix_packing_t{width, cap, returns, inputs};
+    }
+  }
   return PRAGHIP_OK;
 }
 
@@ -459,6 +529,19 @@ hipError_t pack_run(praghip_pack_plan* p, const uint64_t* left, const uint64_t* 
 
 extern "C" {
 
+// packed_target (bfv_acyclic_pack.hpp:53-56): the coefficient a coordinate's
+// constant term reaches after the packing tree over 2^levels leaves, its low
+// `levels` bits reversed, times N >> levels (the reference: 9 levels at
+// N = 16384, spacing 32).
+int praghip_packed_target(size_t coordinate, unsigned levels, uint32_t log_n, uint64_t* target) {
+  if (!target) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (log_n < 1 || log_n > 14 || levels < 1 || levels > log_n) return fail(PRAGHIP_E_SHAPE, "E_PACK_KEY_LEVELS");
+  uint64_t r = 0;
+  for (unsigned j = 0; j < levels; ++j) r = (r << 1) | ((coordinate >> j) & 1);
+  *target = r << (log_n - levels);
+  return PRAGHIP_OK;
+}
+
 int praghip_pack_plan_create(int device, const uint64_t* q, size_t data_primes, uint32_t log_n, size_t dnum,
                              size_t levels, const uint64_t* keys, size_t max_pairs, praghip_pack_plan** plan) {
   if (!plan || !q || !keys) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
@@ -495,12 +578,15 @@ int praghip_pack_plan_create(int device, const uint64_t* q, size_t data_primes, 
   if (e == hipSuccess) e = hipMemcpyAsync(p->kc_dev, &p->kc, sizeof(KsConst), hipMemcpyHostToDevice, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->keys, 2 * levels * key_words * 8, true);
   if (e == hipSuccess) e = hipMemcpyAsync(p->keys, keys, 2 * levels * key_words * 8, hipMemcpyHostToDevice, p->stream);
-  if (e == hipSuccess) {
+  // the fused kernel's running sums and work queue, only for shapes the
+  // three-phase kernels do not take (they never touch either)
+  const bool fused = !keyswitch_rows_supported(p->kc);
+  if (e == hipSuccess && fused) {
     p->acc_slots = ks_acc_slots(int(log_n));
     e = p->acc_slots ? p->buf.alloc((void**)&p->acc, size_t(p->acc_slots) * 2 * n * 8, true) : hipErrorInvalidValue;
   }
-  if (e == hipSuccess) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
-  if (e == hipSuccess) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
+  if (e == hipSuccess && fused) e = p->buf.alloc((void**)&p->queue, kQueueWords * 4, false);
+  if (e == hipSuccess && fused) e = hipMemsetAsync(p->queue, 0, kQueueWords * 4, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->work, 2 * max_pairs * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->ksout, 2 * max_pairs * ct * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->prod, 2 * max_pairs * 2 * K * n * 8, true);
@@ -983,6 +1069,24 @@ int praghip_token_stack_store(praghip_token_plan* p, size_t slot, unsigned level
   return PRAGHIP_OK;
 }
 
+// stack_store waiting on the view's ready event (resident.cu:176-179): the
+// plan's stream waits on `ready`, copies, and the copy is waited for.
+int praghip_token_stack_store_ready(praghip_token_plan* p, size_t slot, unsigned level, const uint64_t* view,
+                                    void* ready) {
+  if (!p) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  const size_t ct = 2 * p->P << p->log_n;
+  if (p->closing || slot >= p->slots || level > p->levels || !view || !ready || !aligned8(view))
+    return fail(PRAGHIP_E_ARGUMENT, "E_DEVICE_STACK_VIEW");
+  uint64_t* dst = p->stack + (slot * (p->levels + 1) + level) * ct;
+  DeviceScope scope(p->device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = hipStreamWaitEvent(p->stream, static_cast<hipEvent_t>(ready), 0);
+  if (e == hipSuccess && view != dst) e = hipMemcpyAsync(dst, view, ct * 8, hipMemcpyDeviceToDevice, p->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  if (e != hipSuccess) return token_failure(p, e, "stack_store");
+  return PRAGHIP_OK;
+}
+
 int praghip_token_stack_view(praghip_token_plan* p, size_t slot, unsigned level, const uint64_t** view) {
   if (!p || !view) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   if (p->closing || slot >= p->slots || level > p->levels) return fail(PRAGHIP_E_ARGUMENT, "E_DEVICE_STACK_INDEX");
@@ -991,12 +1095,15 @@ int praghip_token_stack_view(praghip_token_plan* p, size_t slot, unsigned level,
   return PRAGHIP_OK;
 }
 
-int praghip_token_download(praghip_token_plan* p, const uint64_t* view, uint64_t* output) {
+static int token_download(praghip_token_plan* p, const uint64_t* view, void* ready, bool need_ready,
+                          uint64_t* output) {
   if (!p || !output) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
-  if (p->closing || !view || !in_plan(p, view)) return fail(PRAGHIP_E_ARGUMENT, "E_DEVICE_DOWNLOAD_VIEW");
+  if (p->closing || !view || !in_plan(p, view) || (need_ready && !ready))
+    return fail(PRAGHIP_E_ARGUMENT, "E_DEVICE_DOWNLOAD_VIEW");
   const size_t ct = 2 * p->P << p->log_n;
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
+  if (e == hipSuccess && ready) e = hipStreamWaitEvent(p->stream, static_cast<hipEvent_t>(ready), 0);
   if (e == hipSuccess) e = hipMemcpyAsync(output, view, ct * 8, hipMemcpyDeviceToHost, p->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
   if (e != hipSuccess) {
@@ -1005,6 +1112,15 @@ int praghip_token_download(praghip_token_plan* p, const uint64_t* view, uint64_t
     return token_failure(p, e, "download");
   }
   return PRAGHIP_OK;
+}
+
+int praghip_token_download(praghip_token_plan* p, const uint64_t* view, uint64_t* output) {
+  return token_download(p, view, nullptr, false, output);
+}
+
+// download waiting on the view's ready event (resident.cu:187-189).
+int praghip_token_download_ready(praghip_token_plan* p, const uint64_t* view, void* ready, uint64_t* output) {
+  return token_download(p, view, ready, true, output);
 }
 
 int praghip_token_timing(const praghip_token_plan* p, praghip_timing* out) {

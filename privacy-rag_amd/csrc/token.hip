@@ -177,4 +177,45 @@ hipError_t launch_pack_finish(const uint64_t* a, const uint64_t* b, uint64_t* ou
   return hipGetLastError();
 }
 
+// Selective evaluation of a batch (evaluate_selective, matrix.cu:65-81, with
+// the c0 gather of matrix.cu:41-44): c0 of every output group keeps only the
+// `count` target coefficients idx[] (strictly increasing, < N) and is zero
+// elsewhere; selected[g][k][j] = c0[g][k][idx[j]] when selected is given.  One
+// thread per c0 coefficient finds its coefficient among the targets by binary
+// search over idx staged in LDS; c1 is left as it is.
+__global__ void __launch_bounds__(256)
+    select_c0_kernel(uint64_t* __restrict__ out, size_t groups, int primes, int log_n,
+                     const uint64_t* __restrict__ idx, unsigned count, uint64_t* __restrict__ selected) {
+  __shared__ uint64_t targets[kMaxTargets];
+  for (unsigned j = threadIdx.x; j < count; j += blockDim.x) targets[j] = idx[j];
+  __syncthreads();
+  const size_t n = size_t(1) << log_n, per_group = size_t(primes) << log_n, total = groups * per_group;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += size_t(gridDim.x) * blockDim.x) {
+    const size_t g = i / per_group, r = i % per_group, z = r & (n - 1);
+    unsigned lo = 0, hi = count;  // first target >= z
+    while (lo < hi) {
+      const unsigned mid = (lo + hi) >> 1;
+      if (targets[mid] < z)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    uint64_t* c0 = out + g * 2 * per_group + r;  // c0 limb k, coefficient z
+    if (lo < count && targets[lo] == z) {
+      if (selected) selected[(g * size_t(primes) + (r >> log_n)) * count + lo] = *c0;
+    } else {
+      *c0 = 0;
+    }
+  }
+}
+
+hipError_t launch_select_c0(uint64_t* out, size_t groups, int primes, int log_n, const uint64_t* idx,
+                            unsigned count, uint64_t* selected, hipStream_t s) {
+  if (count == 0 || count > kMaxTargets) return hipErrorInvalidValue;
+  const size_t total = groups * size_t(primes) << log_n;
+  hipLaunchKernelGGL(select_c0_kernel, dim3(elem_grid(total)), dim3(256), 0, s, out, groups, primes, log_n, idx,
+                     count, selected);
+  return hipGetLastError();
+}
+
 }  // namespace praghip

@@ -25,11 +25,11 @@ u64 bit patterns); torch is used only for memory and streams.
 from ._lib import Cleanup, PraghipError, Timing, check, lib  # noqa: F401
 from .ntt import NttBatch, ntt_tables  # noqa: F401
 from .keyswitch import Switch  # noqa: F401
-from .shares import (LocalShares, bfv_delta, dyadic_mac, lift59, local_dot_scale,  # noqa: F401
+from .shares import (LocalShares, ShareStorage, bfv_delta, dyadic_mac, lift59, local_dot_scale,  # noqa: F401
                      local_dot_scale_noalloc, ring_add, ring_layout, ring_scale, ring_sum_rows, share_gemm)
 from .weights import MappedWeights  # noqa: F401
 from .qwen3 import QWEN3_0_6B, Qwen3LocalGemms, Qwen3Shape  # noqa: F401
-from .matrix import Matrix, PublicZero  # noqa: F401
+from .matrix import Matrix, MatrixPacking, PublicZero, matrix_packing  # noqa: F401
 from .token import DeviceCipherBatch, Packing, TokenWeights, packed_target  # noqa: F401
 from . import synth  # noqa: F401
 

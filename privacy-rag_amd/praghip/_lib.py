@@ -40,6 +40,14 @@ class GemmDesc(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("shifts", ctypes.c_void_p), ("y", ctypes.c_void_p),
                 ("m", ctypes.c_size_t), ("k", ctypes.c_size_t), ("n", ctypes.c_size_t),
                 ("w_bits", ctypes.c_int), ("mask_bits", ctypes.c_int)]
+
+
+class MatrixPackingT(ctypes.Structure):
+    """praghip_matrix_packing_t (prag::MatrixPacking, bfv_layout.hpp:8)."""
+    _fields_ = [("reduction", ctypes.c_uint64), ("columns", ctypes.c_uint64), ("returns", ctypes.c_uint64),
+                ("inputs", ctypes.c_uint64)]
+
+
 pp = ctypes.POINTER(ctypes.c_void_p)
 
 SIGNATURES = {
@@ -70,6 +78,13 @@ SIGNATURES = {
     "praghip_ring_scale": (i32, [i32, vp, u64, vp, sz, i32, vp]),
     "praghip_ring_layout": (i32, [i32, vp, sz, vp, vp, sz, vp]),
     "praghip_ring_sum_rows": (i32, [i32, vp, vp, sz, sz, i32, vp]),
+    "praghip_storage_allocate": (i32, [i32, sz, pp]),
+    "praghip_storage_write": (i32, [vp, sz, vp, sz]),
+    "praghip_storage_read": (i32, [vp, sz, sz, vp]),
+    "praghip_storage_data": (i32, [vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t)]),
+    "praghip_storage_stats": (i32, [vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "praghip_storage_clear": (i32, [vp, ctypes.POINTER(Cleanup)]),
+    "praghip_storage_destroy": (None, [vp]),
     "praghip_lift59": (i32, [i32, vp, vp, sz, u32, sz, vp, sz, vp]),
     "praghip_dyadic_mac": (i32, [i32, vp, vp, vp, sz, sz, u32, sz, vp, sz, vp]),
     "praghip_local_dot_workspace_words": (sz, [sz]),
@@ -80,6 +95,8 @@ SIGNATURES = {
     "praghip_matrix_evaluate_device": (i32, [vp, vp, vp, vp]),
     "praghip_matrix_reserve": (i32, [vp, sz]),
     "praghip_matrix_evaluate_device_batch": (i32, [vp, vp, vp, sz, vp]),
+    "praghip_matrix_evaluate_device_batch_selective": (i32, [vp, vp, vp, sz, vp, sz, vp, vp]),
+    "praghip_matrix_packing": (i32, [sz, sz, sz, i32, ctypes.POINTER(MatrixPackingT)]),
     "praghip_matrix_device_bytes": (sz, [vp]),
     "praghip_matrix_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_matrix_destroy": (None, [vp]),
@@ -101,6 +118,8 @@ SIGNATURES = {
     "praghip_token_stack_store": (i32, [vp, sz, ctypes.c_uint, vp, vp]),
     "praghip_token_stack_view": (i32, [vp, sz, ctypes.c_uint, pp]),
     "praghip_token_download": (i32, [vp, vp, vp]),
+    "praghip_token_stack_store_ready": (i32, [vp, sz, ctypes.c_uint, vp, vp]),
+    "praghip_token_download_ready": (i32, [vp, vp, vp, vp]),
     "praghip_token_timing": (i32, [vp, ctypes.POINTER(Timing)]),
     "praghip_token_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_token_destroy": (None, [vp]),
@@ -109,6 +128,7 @@ SIGNATURES = {
     "praghip_pack_pair_device": (i32, [vp, vp, vp, sz, ctypes.c_uint, vp, vp]),
     "praghip_pack_tree_device": (i32, [vp, vp, sz, sz, vp]),
     "praghip_pack_merges": (i32, [vp, ctypes.POINTER(u64)]),
+    "praghip_packed_target": (i32, [sz, ctypes.c_uint, u32, ctypes.POINTER(ctypes.c_uint64)]),
     "praghip_pack_timing": (i32, [vp, ctypes.POINTER(Timing)]),
     "praghip_pack_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_pack_destroy": (None, [vp]),

@@ -3,11 +3,24 @@
 from __future__ import annotations
 
 import ctypes
+from collections import namedtuple
 
 import numpy as np
 
-from ._lib import Cleanup, check, lib, shape_error
+from ._lib import Cleanup, MatrixPackingT, check, lib, shape_error
 from ._util import dev_ptr, host_u64, stream_handle, u64_dtypes
+
+
+MatrixPacking = namedtuple("MatrixPacking", "reduction columns returns inputs")
+
+
+def matrix_packing(batch: int, inner: int, outputs: int, qk_reverse64: bool = False) -> MatrixPacking:
+    """prag::matrix_packing / matrix_packing_qk_reverse64 (bfv_layout.hpp:8-27):
+    the packing of a batch x inner x outputs matrix product that moves the
+    fewest ciphertext bytes.  Raises E_MATRIX_SHAPE / E_QK_REVERSE64_SHAPE."""
+    out = MatrixPackingT()
+    check(lib().praghip_matrix_packing(batch, inner, outputs, int(bool(qk_reverse64)), ctypes.byref(out)))
+    return MatrixPacking(int(out.reduction), int(out.columns), int(out.returns), int(out.inputs))
 
 
 class Matrix:
@@ -57,15 +70,30 @@ class Matrix:
         """Allocates the scratch of evaluate_device_batch for up to `groups` evaluations (once)."""
         check(lib().praghip_matrix_reserve(self._h, groups))
 
-    def evaluate_device_batch(self, rings, out, stream=None):
+    def evaluate_device_batch(self, rings, out, targets=None, selected=None, stream=None):
         """rings: GPU [groups][blocks][2^log_n] words below 2^59 (not checked);
-        out: GPU [groups][2][P][2^log_n]."""
+        out: GPU [groups][2][P][2^log_n].  With `targets` (host, 1..512
+        strictly increasing coefficient indices) the selective form on the
+        device: c0 zero outside the targets, and `selected` (GPU
+        [groups][P][len(targets)] or None) receives the target coefficients of
+        c0 (gather_c0, matrix.cu:41-44)."""
         n = 1 << self.log_n
         groups = rings.numel() // (self.blocks * n)
         if groups * self.blocks * n != rings.numel() or out.numel() != groups * 2 * len(self.q) * n:
             raise shape_error("MATRIX_GPU_SHAPE")
-        check(lib().praghip_matrix_evaluate_device_batch(self._h, dev_ptr(rings, u64_dtypes()),
-                                                         dev_ptr(out, u64_dtypes()), groups, stream_handle(stream)))
+        if targets is None:
+            check(lib().praghip_matrix_evaluate_device_batch(self._h, dev_ptr(rings, u64_dtypes()),
+                                                             dev_ptr(out, u64_dtypes()), groups,
+                                                             stream_handle(stream)))
+            return out
+        t = np.ascontiguousarray(targets, dtype=np.uint64)
+        if selected is not None and selected.numel() != groups * len(self.q) * t.size:
+            raise shape_error("MATRIX_GPU_SHAPE")
+        sp = None if selected is None else dev_ptr(selected, u64_dtypes())
+        check(lib().praghip_matrix_evaluate_device_batch_selective(self._h, dev_ptr(rings, u64_dtypes()),
+                                                                   dev_ptr(out, u64_dtypes()), groups,
+                                                                   t.ctypes.data, t.size, sp,
+                                                                   stream_handle(stream)))
         return out
 
     def device_bytes(self) -> int:

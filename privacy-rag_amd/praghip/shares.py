@@ -186,6 +186,67 @@ def local_dot_scale_noalloc(shares, weights, q, delta, r, out, stream=None):
     return out
 
 
+class ShareStorage:
+    """prag::model::ShareStorage (local_shares.hpp:12-17) from
+    LocalShares.allocate: device words of one participant's shares,
+    zero-filled; write/read are synchronous; clear() wipes and frees."""
+
+    def __init__(self, words: int, device: int = 0, on_clear=None):
+        import ctypes
+        h = ctypes.c_void_p()
+        check(lib().praghip_storage_allocate(device, int(words), ctypes.byref(h)))
+        self._h = h
+        self.words = int(words)
+        self._on_clear = on_clear
+
+    def write(self, offset: int, words) -> None:
+        import numpy as np
+        a = np.ascontiguousarray(words, dtype=np.uint64)
+        check(lib().praghip_storage_write(self._h, int(offset), a.ctypes.data if a.size else None, a.size))
+
+    def read(self, offset: int, count: int):
+        import numpy as np
+        out = np.empty(int(count), dtype=np.uint64)
+        check(lib().praghip_storage_read(self._h, int(offset), int(count), out.ctypes.data if count else None))
+        return out
+
+    @property
+    def data_ptr(self) -> int:
+        """Device address of word 0 (for the device-pointer entry points)."""
+        import ctypes
+        p, n = ctypes.c_void_p(), ctypes.c_size_t()
+        check(lib().praghip_storage_data(self._h, ctypes.byref(p), ctypes.byref(n)))
+        return int(p.value)
+
+    def stats(self):
+        import ctypes
+        up, down = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().praghip_storage_stats(self._h, ctypes.byref(up), ctypes.byref(down)))
+        return {"uploaded_bytes": up.value, "downloaded_bytes": down.value}
+
+    def _released(self):
+        cb, self._on_clear = getattr(self, "_on_clear", None), None
+        if cb is not None:
+            cb(self)
+
+    def clear(self):
+        """ShareStorage::clear: wipe with zeros, synchronise, free (idempotent)."""
+        import ctypes
+        from ._lib import Cleanup
+        c = Cleanup()
+        check(lib().praghip_storage_clear(self._h, ctypes.byref(c)))
+        if c.closed:
+            self._released()
+        return c
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().praghip_storage_destroy(h)
+            self._h = None
+            self._released()
+
+
 class LocalShares:
     """Host-vector mirror of prag::model::LocalShares (local_shares.hpp:22-32).
 
@@ -200,6 +261,7 @@ class LocalShares:
         import torch
         self.device = torch.device("cuda", device)
         self.kernels = self.uploaded_bytes = self.downloaded_bytes = 0
+        self.live_bytes = self.peak_bytes = 0
 
     def _up(self, v):
         import numpy as np
@@ -259,6 +321,19 @@ class LocalShares:
         self.uploaded_bytes += wa.nbytes
         return self._down(share_gemm(xa.view(rows, inner), wt, mask_bits=mask_bits)).reshape(rows, out)
 
+    def allocate(self, words: int) -> ShareStorage:
+        """LocalShares::allocate (local_shares.hpp:29, local_shares.cu:37): a
+        zero-filled device ShareStorage of `words` words (E_CUDA_SHAPE for 0)."""
+        st = ShareStorage(words, self.device.index or 0, on_clear=self._released)
+        self.live_bytes += st.words * 8
+        self.peak_bytes = max(self.peak_bytes, self.live_bytes)
+        return st
+
+    def _released(self, st):
+        self.live_bytes -= st.words * 8
+
     def stats(self):
+        """LocalShareStats (local_shares.hpp:18-21)."""
         return {"kernels": self.kernels, "uploaded_bytes": self.uploaded_bytes,
-                "downloaded_bytes": self.downloaded_bytes}
+                "downloaded_bytes": self.downloaded_bytes, "live_bytes": self.live_bytes,
+                "peak_bytes": self.peak_bytes}

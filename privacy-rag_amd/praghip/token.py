@@ -105,15 +105,20 @@ class TokenWeights:
     def slot_view(self, batch: DeviceCipherBatch, slot: int) -> DeviceCipherBatch:
         return DeviceCipherBatch(batch.data + slot * self.ct_words * 8, self.ct_words, batch.owner)
 
-    def stack_store(self, slot: int, level: int, view, stream=None):
+    def stack_store(self, slot: int, level: int, view, stream=None, ready=None):
         """view: a DeviceCipherBatch of one ciphertext or a GPU tensor of 2 P N
-        words, produced on `stream` (default: torch's current stream)."""
+        words, produced on `stream` (default: torch's current stream); with
+        `ready` (a torch.cuda.Event recorded after the producer's writes) the
+        plan's own stream waits on that event instead (resident.cu:176-179)."""
         if isinstance(view, DeviceCipherBatch):
             words, ptr = view.words, view.data
         else:
             words, ptr = view.numel(), dev_ptr(view, u64_dtypes())
         if words != self.ct_words:
             raise shape_error("E_DEVICE_STACK_VIEW")
+        if ready is not None:
+            check(lib().praghip_token_stack_store_ready(self._h, slot, level, ptr, ready.cuda_event))
+            return
         check(lib().praghip_token_stack_store(self._h, slot, level, ptr, stream_handle(stream)))
 
     def stack_view(self, slot: int, level: int) -> DeviceCipherBatch:
@@ -121,11 +126,15 @@ class TokenWeights:
         check(lib().praghip_token_stack_view(self._h, slot, level, ctypes.byref(v)))
         return DeviceCipherBatch(int(v.value), self.ct_words, self)
 
-    def download(self, view: DeviceCipherBatch) -> np.ndarray:
+    def download(self, view: DeviceCipherBatch, ready=None) -> np.ndarray:
+        """Host copy of a view; with `ready` (torch.cuda.Event) the copy waits on it."""
         if view.words != self.ct_words:
             raise shape_error("E_DEVICE_DOWNLOAD_VIEW")
         out = np.empty((2, len(self.q), 1 << self.log_n), dtype=np.uint64)
-        check(lib().praghip_token_download(self._h, view.data, out.ctypes.data))
+        if ready is not None:
+            check(lib().praghip_token_download_ready(self._h, view.data, ready.cuda_event, out.ctypes.data))
+        else:
+            check(lib().praghip_token_download(self._h, view.data, out.ctypes.data))
         return out
 
     def timing(self) -> Timing:
@@ -148,13 +157,14 @@ class TokenWeights:
             self._h = None
 
 
-def packed_target(coordinate: int, levels: int = 9, spacing: int = 32) -> int:
-    """Coefficient that coordinate lands on after the packing tree: its low
-    `levels` bits reversed, times the spacing (bfv_acyclic_pack.hpp:53-56)."""
-    r = 0
-    for j in range(levels):
-        r = (r << 1) | ((coordinate >> j) & 1)
-    return r * spacing
+def packed_target(coordinate: int, levels: int = 9, log_n: int = 14) -> int:
+    """Coefficient that coordinate lands on after the packing tree
+    (bfv_acyclic_pack.hpp:53-56, praghip_packed_target): its low `levels`
+    bits reversed, times N >> levels (32 for the reference's 9 levels at
+    N = 16384)."""
+    out = ctypes.c_uint64()
+    check(lib().praghip_packed_target(int(coordinate), int(levels), int(log_n), ctypes.byref(out)))
+    return int(out.value)
 
 
 class Packing:

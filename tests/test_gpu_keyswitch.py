@@ -103,6 +103,11 @@ def test_switch_errors_and_cleanup(gpu):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(from_dev(tout), sw.apply(ct))
     t = sw.timing()
+    # sensitive: key [6][2][7][N], products [2][7][N], expanded digits [6][7][N],
+    # staging in and out [2][6][N] each; no fused-kernel scratch at N = 16384
+    assert t.sensitive_bytes == (6 * 2 * 7 + 2 * 7 + 6 * 7 + 2 * 12) * n * 8
+    # public: twiddle tables 7 x N x 48 B (5.25 MiB) and constants
+    assert 7 * n * 48 <= t.device_bytes - t.sensitive_bytes < 7 * n * 48 + (64 << 10)
     c = sw.close()
     assert c.closed and c.first_hip_error == 0
     assert c.wipe_synchronized_bytes == c.freed_bytes == t.sensitive_bytes > 0

@@ -141,6 +141,50 @@ def test_matrix_batch(gpu, log_n, blocks, groups):
     m.close()
 
 
+@pytest.mark.parametrize("targets", ["edges", "max512", "one"])
+def test_matrix_batch_selective(gpu, targets):
+    """The device-side selective batch (evaluate_selective + gather_c0,
+    matrix.cu:41-44,65-81): every group's c0 is the full batch's c0 at the
+    targets and zero elsewhere, c1 is the full batch's, `selected` holds the
+    target coefficients, and group 0 equals the host evaluate_selective."""
+    import torch
+    log_n, blocks, groups, n = 14, 2, 5, 16384
+    print(f"[matrix-selective] targets={targets}", flush=True)
+    q = cf.LOCKED_PRIMES[:6]
+    idx = {"edges": np.array([0, 1, 2, 777, n - 2, n - 1], dtype=np.uint64),
+           "max512": np.arange(512, dtype=np.uint64) * np.uint64(31) + np.uint64(5),
+           "one": np.array([4096], dtype=np.uint64)}[targets]
+    ct = oracle.fill_residues(blocks * 2 * 6, n, q, 600).reshape(blocks, 2, 6, n)
+    rings = oracle.fill_u64(groups * blocks * n, 601).reshape(groups, blocks, n) & np.uint64(T59)
+    m = praghip.Matrix(q, log_n, ct)
+    m.reserve(groups)
+    full = to_dev(np.zeros((groups, 2, 6, n), dtype=np.uint64))
+    m.evaluate_device_batch(to_dev(rings), full)
+    sel_out = to_dev(np.zeros((groups, 2, 6, n), dtype=np.uint64))
+    selected = to_dev(np.zeros((groups, 6, idx.size), dtype=np.uint64))
+    m.evaluate_device_batch(to_dev(rings), sel_out, targets=idx, selected=selected)
+    torch.cuda.synchronize()
+    f, got, gs = from_dev(full), from_dev(sel_out), from_dev(selected)
+    want = f.copy()
+    keep = np.zeros(n, dtype=bool)
+    keep[idx.astype(np.int64)] = True
+    want[:, 0, :, ~keep] = 0
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(gs, f[:, 0][:, :, idx.astype(np.int64)])
+    np.testing.assert_array_equal(got[0], m.evaluate_selective(rings[0], idx))
+    # without `selected`, and the host-side target checks
+    m.evaluate_device_batch(to_dev(rings), sel_out, targets=idx)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(sel_out), want)
+    for bad, code in [(np.array([], dtype=np.uint64), "MATRIX_GPU_TARGET_COUNT"),
+                      (np.arange(513, dtype=np.uint64), "MATRIX_GPU_TARGET_COUNT"),
+                      (np.array([5, 5], dtype=np.uint64), "MATRIX_GPU_TARGET_INDEX"),
+                      (np.array([n], dtype=np.uint64), "MATRIX_GPU_TARGET_INDEX")]:
+        with pytest.raises(praghip.PraghipError, match=code):
+            m.evaluate_device_batch(to_dev(rings), sel_out, targets=bad)
+    m.close()
+
+
 def test_enc0_batch(gpu):
     """evaluate_device_batch: several encryptions in one call against the
     per-encryption entry point and the oracle."""

@@ -134,3 +134,39 @@ def test_weights_upload_feeds_gemm(gpu, tmp_path):
     y = praghip.share_gemm(to_dev(x), dw.view(rows, cols), mask_bits=59)
     _sync()
     np.testing.assert_array_equal(from_dev(y), oracle.share_gemm(x, w, mask_bits=59))
+
+
+def test_share_storage_round_trip_and_clear(gpu):
+    """LocalShares::allocate / ShareStorage (local_shares.hpp:12-17,29): zero
+    on allocation, write/read round trip at offsets, range and word checks,
+    the device words usable by a ring op, clear wipes and frees, the
+    LocalShareStats live/peak bytes."""
+    import torch
+    ls = praghip.LocalShares()
+    st = ls.allocate(1000)
+    assert ls.stats()["live_bytes"] == 8000 == ls.stats()["peak_bytes"]
+    np.testing.assert_array_equal(st.read(0, 1000), np.zeros(1000, dtype=np.uint64))
+    a = oracle.fill_u64(600, 90) & np.uint64(T59)
+    st.write(100, a)
+    np.testing.assert_array_equal(st.read(100, 600), a)
+    np.testing.assert_array_equal(st.read(0, 100), np.zeros(100, dtype=np.uint64))
+    np.testing.assert_array_equal(st.read(700, 300), np.zeros(300, dtype=np.uint64))
+    assert st.stats() == {"uploaded_bytes": 4800, "downloaded_bytes": 8000 + 4800 + 800 + 2400}
+    for bad in [lambda: st.write(900, a[:101]), lambda: st.read(1001, 0), lambda: st.read(500, 501)]:
+        with pytest.raises(praghip.PraghipError, match="E_CUDA_SHAPE"):
+            bad()
+    with pytest.raises(praghip.PraghipError, match="E_CUDA_WORD"):
+        st.write(0, np.array([1 << 59], dtype=np.uint64))
+    # the device words feed the device-pointer ring ops: double words 100..163 in place
+    lib = praghip.lib()
+    assert lib.praghip_ring_add(0, st.data_ptr + 800, st.data_ptr + 800, st.data_ptr + 800, 64, 59, None) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(st.read(100, 64), (a[:64] * np.uint64(2)) & np.uint64(T59))
+    c = st.clear()
+    assert c.closed and c.wipe_synchronized_bytes == c.freed_bytes == 8000
+    assert st.clear().closed  # idempotent
+    assert ls.stats()["live_bytes"] == 0 and ls.stats()["peak_bytes"] == 8000
+    with pytest.raises(praghip.PraghipError, match="E_CUDA_STORAGE_CLOSED"):
+        st.read(0, 1)
+    with pytest.raises(praghip.PraghipError, match="E_CUDA_SHAPE"):
+        ls.allocate(0)

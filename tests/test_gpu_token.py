@@ -120,6 +120,43 @@ def test_token_shapes(gpu, log_n, P, blocks, slots, width):
     tw.close()
 
 
+def test_token_ready_event_views(gpu):
+    """Device views handed over with a ready event (DeviceCipherBatch::ready,
+    resident.hpp:17-20): evaluate_device runs on a side stream, an event is
+    recorded there, and stack_store / download wait on that event on the
+    plan's own stream (resident.cu:176-179,187-189)."""
+    import torch
+    log_n, P, blocks, slots, width = 12, 3, 2, 2, 64
+    n = 1 << log_n
+    print("[token] ready-event views", flush=True)
+    q = cf.primes_below(50, 2 * n, P)
+    ct = _inputs(q, n, blocks, slots, 760)
+    tw = praghip.TokenWeights(q, log_n, ct, width, levels=2)
+    ring = _ring(blocks, width, 761)
+    local = [int(v) & MASK59 for v in oracle.fill_u64(slots, 762)]
+    want = oracle.token_finished(ct, ring, oracle.token_scaled(local, q), q, log_n, width)
+    side = torch.cuda.Stream()
+    dring, dres = to_dev(ring), to_dev(oracle.token_scaled(local, q))
+    out = to_dev(np.zeros((slots, 2, P, n), dtype=np.uint64))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        tw.evaluate_device(dring, out, residues=dres, stream=side)
+        ready = torch.cuda.Event()
+        ready.record(side)
+    tw.stack_store(0, 2, out[1], ready=ready)
+    tw.stack_store(1, 0, out[0], ready=ready)
+    np.testing.assert_array_equal(tw.download(tw.stack_view(0, 2), ready=ready), want[1])
+    np.testing.assert_array_equal(tw.download(tw.stack_view(1, 0), ready=ready), want[0])
+    lib = praghip.lib()
+    assert lib.praghip_token_stack_store_ready(tw._h, 0, 0, out.data_ptr(), None) == praghip._lib.E_ARGUMENT
+    assert b"E_DEVICE_STACK_VIEW" in lib.praghip_last_error()
+    dl = np.empty((2, P, n), dtype=np.uint64)
+    view = tw.stack_view(0, 0)
+    assert lib.praghip_token_download_ready(tw._h, view.data, None, dl.ctypes.data) == praghip._lib.E_ARGUMENT
+    assert b"E_DEVICE_DOWNLOAD_VIEW" in lib.praghip_last_error()
+    tw.close()
+
+
 def test_token_errors(gpu):
     log_n, blocks, width, slots = 12, 2, 64, 2
     n = 1 << log_n
