@@ -449,6 +449,25 @@ int praghip_weights_max_abs(const praghip_weights *w, uint64_t *max_abs);
 int praghip_weights_upload(const praghip_weights *w, int device, int32_t *dst, void *stream);
 void praghip_weights_close(praghip_weights *w);
 
+/* ------------------------------------------------------------- frames */
+/* The 96-byte public frame header of the reference's Channel
+ * (native/src/channel.cpp:122-150): "PRGCF001", session[16], config[32], then
+ * big-endian u64 sequence, payload bytes, stage, operation and version 1.  A
+ * ciphertext frame's payload is the [component][prime][N] little-endian u64
+ * layout of every entry point here (2 x 6 x 16384 x 8 = 1,572,864 bytes for
+ * a full ciphertext).  encode (send_data): out[96].  decode: the fields of a
+ * header with the magic and version 1 (E_FRAME_BINDING otherwise).  check
+ * (recv_data): E_FRAME_BINDING unless every field equals `expect`.  Host
+ * only. */
+typedef struct praghip_frame_header {
+  uint8_t session[16];
+  uint8_t config[32];
+  uint64_t sequence, size, stage, operation;
+} praghip_frame_header;
+int praghip_frame_encode(const praghip_frame_header *header, uint8_t *out);
+int praghip_frame_decode(const uint8_t *in, praghip_frame_header *header);
+int praghip_frame_check(const uint8_t *in, const praghip_frame_header *expect);
+
 /* ------------------------------------------------------ synthetic inputs */
 /* Seeded counter-based inputs (no counterpart in the reference, whose probes
  * draw from mt19937_64, check_resident.cpp:26): element i of the buffer is

@@ -31,7 +31,7 @@ from .weights import MappedWeights  # noqa: F401
 from .qwen3 import QWEN3_0_6B, Qwen3LocalGemms, Qwen3Shape  # noqa: F401
 from .matrix import Matrix, MatrixPacking, PublicZero, matrix_packing  # noqa: F401
 from .token import DeviceCipherBatch, Packing, TokenWeights, packed_target  # noqa: F401
-from . import synth  # noqa: F401
+from . import frames, synth  # noqa: F401
 
 
 def device_count() -> int:

@@ -12,7 +12,7 @@ INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
 OBJ = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libpraghip.so")
 SOURCES = ["ntt.hip", "keyswitch.hip", "keyswitch_rows.hip", "gemm.hip", "elementwise.hip", "shares.hip", "token.hip", "api.cpp",
-           "plans.cpp", "weights.cpp"]
+           "plans.cpp", "weights.cpp", "frames.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Wall", "-Wno-unused-function",
          # packed FP32 instructions are kept out of every kernel

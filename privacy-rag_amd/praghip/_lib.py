@@ -48,6 +48,12 @@ class MatrixPackingT(ctypes.Structure):
                 ("inputs", ctypes.c_uint64)]
 
 
+class FrameHeaderT(ctypes.Structure):
+    """praghip_frame_header (the fields of channel.cpp:126-134)."""
+    _fields_ = [("session", ctypes.c_uint8 * 16), ("config", ctypes.c_uint8 * 32), ("sequence", ctypes.c_uint64),
+                ("size", ctypes.c_uint64), ("stage", ctypes.c_uint64), ("operation", ctypes.c_uint64)]
+
+
 pp = ctypes.POINTER(ctypes.c_void_p)
 
 SIGNATURES = {
@@ -139,6 +145,9 @@ SIGNATURES = {
     "praghip_weights_max_abs": (i32, [vp, ctypes.POINTER(u64)]),
     "praghip_weights_upload": (i32, [vp, i32, vp, vp]),
     "praghip_weights_close": (None, [vp]),
+    "praghip_frame_encode": (i32, [ctypes.POINTER(FrameHeaderT), vp]),
+    "praghip_frame_decode": (i32, [vp, ctypes.POINTER(FrameHeaderT)]),
+    "praghip_frame_check": (i32, [vp, ctypes.POINTER(FrameHeaderT)]),
     "praghip_fill_residues": (i32, [i32, vp, sz, u32, vp, sz, u64, vp]),
     "praghip_fill_u64": (i32, [i32, vp, sz, u64, vp]),
     "praghip_fill_i8": (i32, [i32, vp, sz, u64, vp]),
