@@ -22,6 +22,15 @@
  * After a HIP runtime error a plan releases itself (wipes and frees its
  * buffers) and every later call returns PRAGHIP_E_CLOSED, as the reference's
  * backends do (switch.cu:124, ntt.cu:163-167).
+ *
+ * A plan owns one set of scratch buffers that every call on it uses.  Calls on
+ * one plan must therefore be ordered: device-pointer calls on one stream at a
+ * time, and a host-pointer call (which runs on the plan's own stream) only
+ * after the caller's earlier device calls on that plan have completed.  Two
+ * calls that overlap on one plan - on different streams, or from different
+ * threads - race on that scratch.  This is the reference's single-caller rule
+ * (switch.cu:133, "single-threaded session caller only"); independent plans
+ * may run concurrently.
  */
 #ifndef PRAGHIP_H
 #define PRAGHIP_H

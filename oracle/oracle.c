@@ -186,18 +186,14 @@ void orc_barrett_ratio(uint64_t q, uint64_t *r0, uint64_t *r1) {
   *r0 = (uint64_t)ratio;
   *r1 = (uint64_t)(ratio >> 64);
 }
+/* a*b mod q.  The reference's kernels reduce the 128-bit product with SEAL's
+ * Barrett ratio (switch.cu:30-45); the result is the exact residue, so the
+ * oracle states it directly as a 128-bit remainder (the ratio arguments are
+ * kept for the callers' signatures). */
 static inline uint64_t mul_barrett(uint64_t a, uint64_t b, uint64_t q, uint64_t r0, uint64_t r1) {
-  const uint64_t lo = a * b, hi = mulhi64(a, b);
-  const uint64_t carry0 = mulhi64(lo, r0);
-  const uint64_t round1 = lo * r1;
-  const uint64_t tmp = round1 + carry0;
-  const uint64_t high1 = mulhi64(lo, r1) + (tmp < round1);
-  const uint64_t round2 = hi * r0;
-  const uint64_t next = tmp + round2;
-  const uint64_t high2 = mulhi64(hi, r0) + (next < tmp);
-  const uint64_t quotient = hi * r1 + high1 + high2;
-  const uint64_t rem = lo - quotient * q;
-  return rem >= q ? rem - q : rem;
+  (void)r0;
+  (void)r1;
+  return (uint64_t)(((u128)a * b) % q);
 }
 uint64_t orc_mul_barrett(uint64_t a, uint64_t b, uint64_t q) {
   uint64_t r0, r1;

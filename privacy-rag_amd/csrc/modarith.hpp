@@ -52,22 +52,25 @@ PH_HD uint64_t sub_mod(uint64_t a, uint64_t b, uint64_t q) {
   return x >= q ? x - q : x;
 }
 
-// SEAL barrett_reduce_128 applied to a*b with ratio floor((2^128-1)/q) = (r0, r1).
+// a*b mod q by Barrett reduction of the 128-bit product x = xh 2^64 + xl with
+// the ratio R = floor((2^128-1)/q) = r1 2^64 + r0 (the reduction SEAL uses,
+// which the reference's kernels call at switch.cu:30-45).  The quotient
+// estimate is floor(x R / 2^128): the high word of x R's middle column
+// (xl r1 + xh r0 + hi(xl r0)) carries into its top word
+// (xh r1 + hi(xl r1) + hi(xh r0)); the estimate is at most one below
+// floor(x / q), so x - est q lies in [0, 2q) and is exact in the low word.
 struct Barrett {
   uint64_t q, r0, r1;
 };
 PH_HD uint64_t mul_barrett(uint64_t a, uint64_t b, const Barrett m) {
-  const uint64_t lo = a * b, hi = mulhi64(a, b);
-  const uint64_t carry0 = mulhi64(lo, m.r0);
-  const uint64_t round1 = lo * m.r1;
-  const uint64_t tmp = round1 + carry0;
-  const uint64_t high1 = mulhi64(lo, m.r1) + (tmp < round1);
-  const uint64_t round2 = hi * m.r0;
-  const uint64_t next = tmp + round2;
-  const uint64_t high2 = mulhi64(hi, m.r0) + (next < tmp);
-  const uint64_t quotient = hi * m.r1 + high1 + high2;
-  const uint64_t rem = lo - quotient * m.q;
-  return rem >= m.q ? rem - m.q : rem;
+  const uint64_t xl = a * b, xh = mulhi64(a, b);
+  const uint64_t t0 = xl * m.r1, t1 = xh * m.r0;
+  const uint64_t mid0 = t0 + mulhi64(xl, m.r0);
+  const uint64_t mid1 = mid0 + t1;
+  const uint64_t carries = uint64_t(mid0 < t0) + uint64_t(mid1 < t1);
+  const uint64_t est = xh * m.r1 + mulhi64(xl, m.r1) + mulhi64(xh, m.r0) + carries;
+  const uint64_t r = xl - est * m.q;
+  return r >= m.q ? r - m.q : r;
 }
 
 // floor(w 2^64 / q) for w < q, from the Barrett ratio R = floor((2^128-1)/q):

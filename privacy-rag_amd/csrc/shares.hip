@@ -216,8 +216,11 @@ __global__ void __launch_bounds__(256) local_scale_kernel(const uint64_t* __rest
   if (threadIdx.x < unsigned(sc.count)) {
     const unsigned k = threadIdx.x;
     const uint64_t m = sum & ((1ull << 59) - 1);
-    const uint64_t lo = m * sc.r, hi = __umul64hi(m, sc.r), added = lo + (1ull << 58);
-    const uint64_t fix = ((hi + (added < lo ? 1 : 0)) << 5) | (added >> 59);  // < 2^59 + 1
+    // floor((r m + 2^58) / 2^59) of the 128-bit r m: add the half to the low
+    // word, carry into the high word, keep bits 59..122
+    const uint64_t rm_lo = m * sc.r, rm_hi = __umul64hi(m, sc.r);
+    const uint64_t half_lo = rm_lo + (1ull << 58), half_hi = rm_hi + (half_lo < rm_lo ? 1 : 0);
+    const uint64_t fix = (half_hi << 5) | (half_lo >> 59);  // < 2^59 + 1
     const Barrett b = sc.m[k];
     const uint64_t z = mul_barrett(m, sc.delta[k], b);
     scaled[slot * unsigned(sc.count) + k] = add_mod(z, fix % b.q, b.q);
