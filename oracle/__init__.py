@@ -61,7 +61,7 @@ def lib():
             "orc_dyadic_mac": (None, [vp, vp, vp, sz, sz, sz, sz, vp, sz]),
             "orc_local_dot_scale": (None, [vp, vp, sz, sz, vp, u64, vp, sz, vp]),
             "orc_lift59_blocks": (None, [vp, vp, sz, sz, sz, vp, sz]),
-            "orc_enc0": (i32, [vp, vp, vp, vp, sz, ctypes.c_uint, vp, vp, vp]),
+            "orc_enc0": (i32, [vp, vp, vp, vp, sz, ctypes.c_uint, vp, vp, vp, i32]),
             "orc_ring_add": (None, [vp, vp, vp, sz, i32]),
             "orc_ring_scale": (None, [vp, u64, vp, sz, i32]),
             "orc_ring_layout": (None, [vp, sz, vp, vp, sz]),
@@ -294,7 +294,7 @@ def matrix_product(ct: np.ndarray, ring: np.ndarray, q, log_n: int, threads: int
     return ntt(acc, t, inverse=True, threads=threads).reshape(2, P, n)
 
 
-def enc0(samples: np.ndarray, pk: np.ndarray, q, log_n: int) -> np.ndarray:
+def enc0(samples: np.ndarray, pk: np.ndarray, q, log_n: int, threads: int = 0) -> np.ndarray:
     """PublicZero::evaluate (enc0.cu:99-114): samples [3][K][N] (u, e0, e1 residues), pk [2][K][N]
     NTT form -> ModDown(INTT(NTT(u) * pk_c) + e_c) [2][K-1][N]."""
     q = _u64(q)
@@ -304,7 +304,7 @@ def enc0(samples: np.ndarray, pk: np.ndarray, q, log_n: int) -> np.ndarray:
     s = _u64(samples)
     k = _u64(pk)
     out = np.empty((2, K - 1, n), dtype=np.uint64)
-    rc = lib().orc_enc0(_p(s), _p(k), _p(out), _p(q), K - 1, log_n, _p(t.fwd), _p(t.inv), _p(t.invn))
+    rc = lib().orc_enc0(_p(s), _p(k), _p(out), _p(q), K - 1, log_n, _p(t.fwd), _p(t.inv), _p(t.invn), threads)
     assert rc == 0
     return out
 

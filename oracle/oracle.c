@@ -202,47 +202,66 @@ uint64_t orc_mul_barrett(uint64_t a, uint64_t b, uint64_t q) {
 }
 
 /* ------------------------------------------------------------------------ */
-/* Negacyclic NTT / INTT, radix-2, stage by stage exactly as the reference    */
-/* launches them (ntt.cu:111-116 driving stage() ntt.cu:42-53):              */
+/* Negacyclic NTT / INTT, radix-2, stage by stage as the reference launches  */
+/* them (ntt.cu:111-116 driving stage() ntt.cu:42-53):                        */
 /*   forward stage l: gap = N>>(l+1), root = fwd[(1<<l) + group] (CT);        */
 /*   inverse stage l: gap = 1<<l, root = inv[N-(N>>l)+1+group] (GS), and the  */
 /*   last stage multiplies both outputs by N^-1.                               */
+/* The loops run group by group (no division per butterfly) and keep Harvey's */
+/* lazy ranges - forward values in [0, 4q), inverse in [0, 2q), with the      */
+/* Shoup product a*w - floor(a*w'/2^64)*q in [0, 2q) for any a < 2^64 -, then */
+/* reduce to canonical once at the end: every stage is exact mod q, so the   */
+/* canonical outputs are the reference's.                                     */
 /* ------------------------------------------------------------------------ */
+static inline uint64_t shoup_lazy(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
+  return a * w - mulhi64(a, wq) * q;
+}
 void orc_ntt_forward(uint64_t *a, unsigned log_n, uint64_t q, const uint64_t *fwd_pairs) {
   const size_t n = (size_t)1 << log_n;
+  const uint64_t q2 = 2 * q;
   for (unsigned l = 0; l < log_n; ++l) {
-    const size_t gap = n >> (l + 1), root_start = (size_t)1 << l;
-    for (size_t j = 0; j < n / 2; ++j) {
-      const size_t group = j / gap, offset = j % gap;
-      const size_t x = group * 2 * gap + offset, y = x + gap;
-      const uint64_t *r = fwd_pairs + 2 * (root_start + group);
-      const uint64_t t = mul_shoup(a[y], r[0], r[1], q);
-      const uint64_t u = a[x];
-      a[x] = add_mod(u, t, q);
-      a[y] = sub_mod(u, t, q);
+    const size_t gap = n >> (l + 1), groups = (size_t)1 << l;
+    for (size_t g = 0; g < groups; ++g) {
+      const uint64_t w = fwd_pairs[2 * (groups + g)], wq = fwd_pairs[2 * (groups + g) + 1];
+      uint64_t *x = a + 2 * g * gap, *y = x + gap;
+      for (size_t j = 0; j < gap; ++j) {
+        const uint64_t u = x[j] >= q2 ? x[j] - q2 : x[j];
+        const uint64_t t = shoup_lazy(y[j], w, wq, q);
+        x[j] = u + t;
+        y[j] = u - t + q2;
+      }
     }
+  }
+  for (size_t i = 0; i < n; ++i) {
+    const uint64_t v = a[i] >= q2 ? a[i] - q2 : a[i];
+    a[i] = v >= q ? v - q : v;
   }
 }
 void orc_ntt_inverse(uint64_t *a, unsigned log_n, uint64_t q, const uint64_t *inv_pairs,
                      const uint64_t *invn_pair) {
   const size_t n = (size_t)1 << log_n;
+  const uint64_t q2 = 2 * q;
   for (unsigned l = 0; l < log_n; ++l) {
-    const size_t gap = (size_t)1 << l, root_start = n - (n >> l) + 1;
+    const size_t gap = (size_t)1 << l, groups = n >> (l + 1), root_start = n - (n >> l) + 1;
     const int last = (l + 1 == log_n);
-    for (size_t j = 0; j < n / 2; ++j) {
-      const size_t group = j / gap, offset = j % gap;
-      const size_t x = group * 2 * gap + offset, y = x + gap;
-      const uint64_t *r = inv_pairs + 2 * (root_start + group);
-      const uint64_t u = a[x], v = a[y];
-      uint64_t s = add_mod(u, v, q), d = mul_shoup(sub_mod(u, v, q), r[0], r[1], q);
-      if (last) {
-        s = mul_shoup(s, invn_pair[0], invn_pair[1], q);
-        d = mul_shoup(d, invn_pair[0], invn_pair[1], q);
+    for (size_t g = 0; g < groups; ++g) {
+      const uint64_t w = inv_pairs[2 * (root_start + g)], wq = inv_pairs[2 * (root_start + g) + 1];
+      uint64_t *x = a + 2 * g * gap, *y = x + gap;
+      for (size_t j = 0; j < gap; ++j) {
+        const uint64_t u = x[j], v = y[j];
+        uint64_t s = u + v;
+        s = s >= q2 ? s - q2 : s;
+        uint64_t d = shoup_lazy(u - v + q2, w, wq, q);
+        if (last) {
+          s = shoup_lazy(s, invn_pair[0], invn_pair[1], q);
+          d = shoup_lazy(d, invn_pair[0], invn_pair[1], q);
+        }
+        x[j] = s;
+        y[j] = d;
       }
-      a[x] = s;
-      a[y] = d;
     }
   }
+  for (size_t i = 0; i < n; ++i) a[i] = a[i] >= q ? a[i] - q : a[i];
 }
 /* NttBatch::transform (ntt.cu:104-127) over a [limbs][N] buffer whose limb l
  * uses prime index l % primes.  Tables are [primes][N][2] / [primes][2]. */
@@ -431,12 +450,19 @@ int orc_keyswitch(const uint64_t *in, uint64_t *out, const uint64_t *key, size_t
 /*   P_c = INTT(NTT(u) (.) pk_c) + e_c,  out_c = ModDown_p(P_c)  [2][L][N].    */
 /* ------------------------------------------------------------------------ */
 int orc_enc0(const uint64_t *samples, const uint64_t *pk, uint64_t *out, const uint64_t *q, size_t L,
-             unsigned log_n, const uint64_t *fwd, const uint64_t *inv, const uint64_t *invn) {
+             unsigned log_n, const uint64_t *fwd, const uint64_t *inv, const uint64_t *invn, int threads) {
   const size_t K = L + 1, n = (size_t)1 << log_n;
   uint64_t *u = (uint64_t *)malloc(K * n * 8), *prod = (uint64_t *)malloc(2 * K * n * 8);
   if (!u || !prod) { free(u); free(prod); return -2; }
   memcpy(u, samples, K * n * 8);
+#ifdef _OPENMP
+  if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+#endif
   for (size_t t = 0; t < K; ++t) orc_ntt_forward(u + t * n, log_n, q[t], fwd + 2 * t * n);
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) schedule(dynamic, 1) num_threads(threads)
+#endif
   for (size_t comp = 0; comp < 2; ++comp)
     for (size_t t = 0; t < K; ++t) {
       uint64_t r0, r1;
@@ -448,6 +474,9 @@ int orc_enc0(const uint64_t *samples, const uint64_t *pk, uint64_t *out, const u
       for (size_t k = 0; k < n; ++k) dst[k] = add_mod(dst[k], e[k], q[t]);
     }
   const uint64_t p = q[L], half = p >> 1;
+#ifdef _OPENMP
+#pragma omp parallel for collapse(2) schedule(dynamic, 1) num_threads(threads)
+#endif
   for (size_t comp = 0; comp < 2; ++comp)
     for (size_t i = 0; i < L; ++i) {
       const uint64_t qi = q[i];
@@ -463,6 +492,7 @@ int orc_enc0(const uint64_t *samples, const uint64_t *pk, uint64_t *out, const u
     }
   free(u);
   free(prod);
+  (void)threads;
   return 0;
 }
 
