@@ -129,7 +129,7 @@ def bench_keyswitch(torch, praghip, steps, warmup, reference=False):
         "batch": batch, "dnum": dnum, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None if reference else measured_traffic("keyswitch", 1),
+                     "traffic": measured_traffic("keyswitch_reference" if reference else "keyswitch", 1),
                      "kernel": "whole keyswitch batch (all its launches); traffic is per batch",
                      "algorithmic_bytes_per_batch": batch * bytes_per_ks,
                      "algorithmic_bytes_per_keyswitch": bytes_per_ks},
@@ -152,11 +152,50 @@ def bench_gemm(torch, praghip, steps, warmup):
     ms = Timer(torch).run(step, steps, warmup)
     tops = 2 * m * k * n / (ms * 1e-3) / 1e12
     mfma_tops = 8 * tops  # eight i8 digit products per u64 x i8 product
+    # the same product on VALU dot products (v_dot4_i32_i8 on the same digit
+    # planes): the alternative the MFMA kernel is measured against
+    y_valu = torch.empty_like(y)
+    ms_valu = Timer(torch).run(lambda: praghip.share_gemm_valu(x, w, y=y_valu), max(1, steps // 2), 2)
+    assert torch.equal(y_valu, y), "VALU and MFMA share GEMMs differ"
     return {
         "shape": [m, k, n], "ms_per_step": ms, "tops": tops,
+        "valu_form": {"ms_per_step": ms_valu, "tops": 2 * m * k * n / (ms_valu * 1e-3) / 1e12,
+                      "kernel": "share_gemm_valu_kernel (v_dot4_i32_i8, same digit planes)",
+                      "mfma_speedup": ms_valu / ms},
         "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm", 1),
                      "kernel": "share_gemm_dma_kernel (i8 MFMA ops executed)"},
+        "_tensors": (x, w, y),
+    }
+
+
+def bench_gemm_f12(torch, praghip, steps, warmup):
+    """C4's shape with the reference's own weights: int32 f12, |w| <= 2^20
+    (quantize_weights.py:91,102), split once into three signed-byte planes
+    (the split is outside the timed region, as weights are static); one launch
+    of the i8-MFMA kernel covers the three planes."""
+    from praghip import synth
+    m, k, n = 512, 1024, 3072
+    x = torch.empty(m * k, dtype=torch.int64, device="cuda").view(m, k)
+    raw = torch.empty(n * k, dtype=torch.int64, device="cuda")
+    y = torch.empty((m, n), dtype=torch.int64, device="cuda")
+    synth.fill_u64(x, 0x5052414700000014)
+    synth.fill_u64(raw, 0x5052414700000114)
+    w = ((raw.view(n, k) & ((1 << 21) - 1)) - (1 << 20)).to(torch.int32)  # in [-2^20, 2^20)
+    planes = praghip.split_weights(w)
+
+    def step():
+        praghip.share_gemm(x, planes, y=y)
+
+    ms = Timer(torch).run(step, steps, warmup)
+    tops = 2 * m * k * n / (ms * 1e-3) / 1e12
+    mfma_tops = 24 * tops  # eight share digits x three weight planes per u64 x f12 product
+    return {
+        "shape": [m, k, n], "weights": "int32 f12, |w| <= 2^20, pre-split into 3 int8 planes",
+        "ms_per_step": ms, "tops": tops,
+        "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm_f12", 1),
+                     "kernel": "share_gemm_dma_kernel, 3 weight planes (i8 MFMA ops executed)"},
         "_tensors": (x, w, y),
     }
 
@@ -352,6 +391,20 @@ def cpu_baselines(torch, res, budget_s: float):
     out["keyswitch_parity"] = bool(np.array_equal(got, gpu_slice))
     out["keyswitch"] = {"value": nb / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
                         "sample": f"{nb} of the 64 N=16384 ciphertexts (dnum=3) with their own keys"}
+    # keyswitch at the reference shape (dnum = 6, the locked 60-bit primes):
+    # the sampled ciphertexts with their keys, parity against the GPU output
+    if "keyswitch_reference" in res and "_sample" in res["keyswitch_reference"]:
+        sm = res["keyswitch_reference"]["_sample"]
+        nb = sm["ct"].shape[0]
+        tab6 = oracle.Tables(sm["q"], LOG_N)
+        t0 = time.perf_counter()
+        got = oracle.keyswitch(sm["ct"], sm["keys"], sm["q"], 6, LOG_N, 1, tables=tab6, per_ct_keys=True,
+                               threads=threads)
+        dt = time.perf_counter() - t0
+        out["keyswitch_reference_parity"] = bool(np.array_equal(got, sm["out"]))
+        out["keyswitch_reference"] = {"value": nb / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
+                                      "sample": f"{nb} of the 64 N=16384 ciphertexts (dnum=6, locked primes) "
+                                                "with their own keys"}
     # GEMM: 64 rows of the 512x1024 activations against all 3072 weight rows
     x_t, w_t, y_t = res["gemm"]["_tensors"]
     rows = 64
@@ -363,6 +416,19 @@ def cpu_baselines(torch, res, budget_s: float):
     out["gemm_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
     out["gemm"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
                    "sample": f"{rows} of 512 activation rows x 1024 x 3072"}
+    # f12 GEMM: 16 activation rows against the int32 weights, parity with the
+    # pre-split GPU product
+    if "gemm_f12" in res and "_tensors" in res["gemm_f12"]:
+        x_t, w_t, y_t = res["gemm_f12"]["_tensors"]
+        rows = 16
+        x = x_t[:rows].cpu().numpy().view(np.uint64)
+        w = w_t.cpu().numpy()
+        t0 = time.perf_counter()
+        y = oracle.share_gemm(x, w, threads=threads)
+        dt = time.perf_counter() - t0
+        out["gemm_f12_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
+        out["gemm_f12"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads,
+                           "kind": "port", "sample": f"{rows} of 512 activation rows x 1024 x 3072, int32 weights"}
     # token tile: two coordinates' columns (resident inputs transformed once,
     # as the GPU plan does at creation) and one level-0 merge, scaled to the
     # tile's 512 columns and 2,044 merges
@@ -436,8 +502,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "keyswitch_dnum3", "keyswitch_dnum6", "gemm", "qwen3",
-                                       "token", "matrix", "enc0", "copy"],
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "keyswitch_dnum3", "keyswitch_dnum6", "gemm",
+                                       "gemm_f12", "qwen3", "token", "matrix", "enc0", "copy"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of oracle NTT timing")
@@ -446,6 +512,7 @@ def main() -> int:
         print(f"bench.py measures one GPU: praghip has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
+    import numpy as np
     import torch
 
     import praghip
@@ -469,12 +536,24 @@ def main() -> int:
     if args.only in ("all", "keyswitch", "keyswitch_dnum6"):
         log("keyswitch N=16384 dnum=6, locked 60-bit primes (the reference shape), 64 ciphertexts ...")
         res["keyswitch_reference"] = bench_keyswitch(torch, praghip, args.steps, args.warmup, reference=True)
-        res["keyswitch_reference"].pop("_tensors")
+        ct_t, keys_t, out_t, qr = res["keyswitch_reference"].pop("_tensors")
+        if not args.no_cpu and args.only == "all":
+            # a few ciphertexts with their keys, on the host, for the CPU leg
+            nb, cw, kw = 8, 2 * 6 * N, 6 * 2 * 7 * N
+            host = lambda t, w: t[: nb * w].cpu().numpy().view(np.uint64).copy()  # noqa: E731
+            res["keyswitch_reference"]["_sample"] = {"ct": host(ct_t, cw).reshape(nb, 2, 6, N),
+                                                     "keys": host(keys_t, kw).reshape(nb, 6, 2, 7, N),
+                                                     "out": host(out_t, cw).reshape(nb, 2, 6, N), "q": qr}
+        del ct_t, keys_t, out_t
         log(f"keyswitch (reference shape) {res['keyswitch_reference']['keyswitch_per_s']:.4g}/s")
     if args.only in ("all", "gemm"):
         log("share GEMM 512x1024x3072 ...")
         res["gemm"] = bench_gemm(torch, praghip, args.steps, args.warmup)
         log(f"GEMM {res['gemm']['tops']:.4g} TOPS")
+    if args.only in ("all", "gemm_f12"):
+        log("share GEMM 512x1024x3072, f12 weights pre-split into 3 planes ...")
+        res["gemm_f12"] = bench_gemm_f12(torch, praghip, args.steps, args.warmup)
+        log(f"GEMM f12 {res['gemm_f12']['tops']:.4g} TOPS")
     if args.only in ("all", "qwen3"):
         log("Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens ...")
         res["qwen3"] = bench_qwen3(torch, praghip, args.steps, args.warmup)
@@ -515,16 +594,16 @@ def main() -> int:
     def clean(d):
         return {k: v for k, v in d.items() if not k.startswith("_")}
 
-    key = next(k for k in ("ntt", "keyswitch", "keyswitch_reference", "gemm", "qwen3", "token", "matrix", "enc0")
-               if k in res)
+    key = next(k for k in ("ntt", "keyswitch", "keyswitch_reference", "gemm", "gemm_f12", "qwen3", "token", "matrix",
+                           "enc0") if k in res)
     primary = res[key]
     value = {"ntt": lambda r: r["ntt_per_s"], "keyswitch": lambda r: r["keyswitch_per_s"],
              "keyswitch_reference": lambda r: r["keyswitch_per_s"],
-             "gemm": lambda r: r["tops"], "qwen3": lambda r: r["tops"],
+             "gemm": lambda r: r["tops"], "gemm_f12": lambda r: r["tops"], "qwen3": lambda r: r["tops"],
              "token": lambda r: r["coordinates_per_s"], "matrix": lambda r: r["evaluations_per_s"],
              "enc0": lambda r: r["encryptions_per_s"]}[key](primary)
     unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "keyswitch_reference": "keyswitch/s", "gemm": "TOPS",
-            "qwen3": "TOPS",
+            "gemm_f12": "TOPS", "qwen3": "TOPS",
             "token": "coordinates/s", "matrix": "evaluations/s", "enc0": "encryptions/s"}[key]
     line = {
         "metric": METRIC,
@@ -537,7 +616,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"gemm": "i8", "qwen3": "i8"}.get(key, "u64"),
+        "dtype": {"gemm": "i8", "gemm_f12": "i8", "qwen3": "i8"}.get(key, "u64"),
         "data": "synthetic (seeded splitmix64 on the GPU)",
         "config": {"workload": {
             "ntt": "batched forward+inverse negacyclic NTT, N=16384, 6 primes ~50 bit, "
@@ -546,6 +625,7 @@ def main() -> int:
             "keyswitch_reference": "keyswitch N=16384, six locked 60-bit primes + special, dnum=6, 64 ciphertexts, "
                                    "64 keys",
             "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64",
+            "gemm_f12": "share GEMM u64[512x1024] x int32 f12[3072x1024]^T mod 2^64 (pre-split weights)",
             "qwen3": "Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens",
             "token": "token-resident tile, 512 coordinates x 4 slots, 19 blocks of 8192, 9-level packing",
             "matrix": "HE matrix product, N=16384, 6 primes, 3 blocks, 64 output groups",

@@ -146,12 +146,28 @@ void praghip_switch_destroy(praghip_switch_plan *plan);
  * (local_shares.hpp:22-32): y[m][n] = ((sum_k x[m][k] * w[n][k]) << shifts[n])
  * mod 2^mask_bits, x u64 device [M][K], w signed device [N][K] (w_bits 8: int8;
  * 32: int32 in [-0x808080, 0x7F7F7F], three balanced signed bytes; the
- * reference f12 domain is |w| <= 2^20),
+ * reference f12 domain is |w| <= 2^20; 24: the same weights pre-split by
+ * praghip_weights_split or praghip_weights_upload_split into three int8
+ * planes [3][N][K], w = sum_e plane_e 256^e - the fast form of static f12
+ * weights),
  * shifts device int8 [N] in [0,63] or NULL, y u64 device [M][N]; mask_bits 59
  * is the reference ring, 64 is no mask.  Asynchronous on `stream` (NULL: the
  * null stream of `device`). */
 int praghip_share_gemm(int device, const uint64_t *x, const void *w, int w_bits, const int8_t *shifts,
                        uint64_t *y, size_t m, size_t k, size_t n, int mask_bits, void *stream);
+
+/* praghip_share_gemm with int8 weights (w_bits 8) computed by VALU dot products
+ * (v_dot4_i32_i8 on the same offset-binary digit planes) instead of the i8
+ * matrix cores: the same results, kept as the measured alternative that the
+ * MFMA kernels are chosen over (bfv_matrix.inc:101-105 is the operation). */
+int praghip_share_gemm_valu(int device, const uint64_t *x, const int8_t *w, const int8_t *shifts, uint64_t *y,
+                            size_t m, size_t k, size_t n, int mask_bits, void *stream);
+
+/* Splits `count` int32 weights in [-0x808080, 0x7F7F7F] (device) into the
+ * three balanced signed-byte planes of w_bits 24 (device int8 [3][count]),
+ * once per weight matrix (the reference's weights are static,
+ * quantize_weights.py:91,102).  Weights outside the range are not detected. */
+int praghip_weights_split(int device, const int32_t *w, int8_t *planes, size_t count, void *stream);
 
 /* A list of share GEMMs launched in order on one stream, for the per-layer
  * projections of Transformer::project_many / project_joint_many
@@ -456,6 +472,11 @@ const int32_t *praghip_weights_data(const praghip_weights *w);
 int praghip_weights_at(const praghip_weights *w, size_t row, size_t col, uint64_t *word);
 int praghip_weights_max_abs(const praghip_weights *w, uint64_t *max_abs);
 int praghip_weights_upload(const praghip_weights *w, int device, int32_t *dst, void *stream);
+/* The file's weights split on the host into the three signed-byte planes of
+ * praghip_share_gemm's w_bits 24 and copied to dst (device int8
+ * [3][rows][cols]); waits for the copy.  E_WEIGHT_RANGE when a weight lies
+ * outside [-0x808080, 0x7F7F7F]. */
+int praghip_weights_upload_split(const praghip_weights *w, int device, int8_t *dst, void *stream);
 void praghip_weights_close(praghip_weights *w);
 
 /* ------------------------------------------------------------- frames */

@@ -21,6 +21,9 @@
 namespace praghip {
 hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
                              int M, int K, int N, int mask_bits, hipStream_t s);
+hipError_t launch_weight_split(const int32_t* w, int8_t* planes, size_t count, hipStream_t s);
+hipError_t launch_share_gemm_valu(const uint64_t* x, const int8_t* w, const int8_t* shifts, uint64_t* y, int M,
+                                  int K, int N, int mask_bits, hipStream_t s);
 }
 
 using namespace praghip;
@@ -743,7 +746,7 @@ int praghip_share_gemm(int device, const uint64_t* x, const void* w, int w_bits,
                        size_t m, size_t k, size_t n, int mask_bits, void* stream) {
   if (m == 0 || n == 0) return PRAGHIP_OK;
   if (!x || !w || !y) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
-  if (w_bits != 8 && w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
+  if (w_bits != 8 && w_bits != 24 && w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
   if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
   if (k >= (1u << 17) || m >= (1u << 31) || n >= (1u << 31)) return fail(PRAGHIP_E_SHAPE, "E_SHARE_SHAPE");
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7 ||
@@ -757,6 +760,33 @@ int praghip_share_gemm(int device, const uint64_t* x, const void* w, int w_bits,
   return PRAGHIP_OK;
 }
 
+int praghip_share_gemm_valu(int device, const uint64_t* x, const int8_t* w, const int8_t* shifts, uint64_t* y,
+                            size_t m, size_t k, size_t n, int mask_bits, void* stream) {
+  if (m == 0 || n == 0) return PRAGHIP_OK;
+  if (!x || !w || !y) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (mask_bits < 1 || mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
+  if (k >= (1u << 17) || m >= (1u << 31) || n >= (1u << 31)) return fail(PRAGHIP_E_SHAPE, "E_SHARE_SHAPE");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7)
+    return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess)
+    e = launch_share_gemm_valu(x, w, shifts, y, int(m), int(k), int(n), mask_bits, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_SHARE_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
+int praghip_weights_split(int device, const int32_t* w, int8_t* planes, size_t count, void* stream) {
+  if (count == 0) return PRAGHIP_OK;
+  if (!w || !planes) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (reinterpret_cast<uintptr_t>(w) & 3) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
+  DeviceScope scope(device);
+  hipError_t e = scope.status();
+  if (e == hipSuccess) e = launch_weight_split(w, planes, count, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_SHARE_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
 int praghip_share_gemm_batch(int device, const praghip_gemm_desc* list, size_t count, void* stream) {
   if (count == 0) return PRAGHIP_OK;
   if (!list) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
@@ -764,7 +794,7 @@ int praghip_share_gemm_batch(int device, const praghip_gemm_desc* list, size_t c
     const praghip_gemm_desc& d = list[i];
     if (d.m == 0 || d.n == 0) continue;
     if (!d.x || !d.w || !d.y) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
-    if (d.w_bits != 8 && d.w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
+    if (d.w_bits != 8 && d.w_bits != 24 && d.w_bits != 32) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_WEIGHT_DTYPE");
     if (d.mask_bits < 1 || d.mask_bits > 64) return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_MASK");
     if (d.k >= (1u << 17) || d.m >= (1u << 31) || d.n >= (1u << 31)) return fail(PRAGHIP_E_SHAPE, "E_SHARE_SHAPE");
     if ((reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.y)) & 7 ||

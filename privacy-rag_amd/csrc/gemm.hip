@@ -224,6 +224,110 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
+// ------------------------------------------------------------- VALU form
+// The same product with VALU dot products instead of the matrix cores: the
+// tiles are staged exactly as in share_gemm_kernel (digit planes of the
+// offset-binary share bytes, int8 weight rows), and each thread forms a 4 x 4
+// block of outputs with v_dot4_i32_i8, one per (row, column, digit) and four
+// k.  It exists as the measured alternative to the MFMA kernels (int8
+// weights).
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    share_gemm_valu_kernel(const uint64_t* __restrict__ x, const int8_t* __restrict__ w,
+                           const int8_t* __restrict__ shifts, uint64_t* __restrict__ y, int M, int K, int N,
+                           uint64_t mask, int w_vec) {
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM][kPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t w_lds[kBN][kPitch];
+  __shared__ int csum[kThreads];
+  const int t = threadIdx.x;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int ar = t >> 3, ak = (t & 7) * 8, wr = t >> 1, wk = (t & 1) * 32;
+  const int rg = t >> 5, cg = t & 31;  // rows rg + 8i, columns cg + 32j
+  int colsum = 0;
+  int acc[4][4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[i][j][d] = 0;
+  const bool x_row_ok = (m0 + ar) < M, w_row_ok = (n0 + wr) < N;
+  const uint64_t* xrow = x + size_t(m0 + ar) * K;
+  const size_t wrow_off = size_t(n0 + wr) * K;
+  TileRegs tr;
+  load_tile<8>(tr, xrow, x_row_ok, w, wrow_off, w_row_ok, 0, K, ak, wk, 0, w_vec);
+  for (int k0 = 0; k0 < K; k0 += kBK) {
+    uint32_t d[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      d[2 * e] = uint32_t(tr.xs[e]) ^ 0x80808080u;
+      d[2 * e + 1] = uint32_t(tr.xs[e] >> 32) ^ 0x80808080u;
+    }
+    uint32_t o[4][4];
+    transpose4(d[0], d[2], d[4], d[6], o[0][0], o[0][1], o[0][2], o[0][3]);
+    transpose4(d[8], d[10], d[12], d[14], o[1][0], o[1][1], o[1][2], o[1][3]);
+    transpose4(d[1], d[3], d[5], d[7], o[2][0], o[2][1], o[2][2], o[2][3]);
+    transpose4(d[9], d[11], d[13], d[15], o[3][0], o[3][1], o[3][2], o[3][3]);
+#pragma unroll
+    for (int dg = 0; dg < 4; ++dg) {
+      *reinterpret_cast<uint2*>(&a_lds[dg][ar][ak]) = make_uint2(o[0][dg], o[1][dg]);
+      *reinterpret_cast<uint2*>(&a_lds[dg + 4][ar][ak]) = make_uint2(o[2][dg], o[3][dg]);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) colsum = __builtin_amdgcn_sdot4(int(tr.wb[q]), 0x01010101, colsum, false);
+    *reinterpret_cast<uint4*>(&w_lds[wr][wk]) = make_uint4(tr.wb[0], tr.wb[1], tr.wb[2], tr.wb[3]);
+    *reinterpret_cast<uint4*>(&w_lds[wr][wk + 16]) = make_uint4(tr.wb[4], tr.wb[5], tr.wb[6], tr.wb[7]);
+    __syncthreads();
+#pragma unroll 1
+    for (int kk = 0; kk < kBK; kk += 4) {
+      int wv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[j] = *reinterpret_cast<const int*>(&w_lds[cg + 32 * j][kk]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int dg = 0; dg < 8; ++dg) {
+          const int xv = *reinterpret_cast<const int*>(&a_lds[dg][rg + 8 * i][kk]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j][dg] = __builtin_amdgcn_sdot4(xv, wv[j], acc[i][j][dg], false);
+        }
+      }
+    }
+    __syncthreads();
+    // the next step's tile is loaded after the dot products (the 128
+    // accumulators leave no registers to hold it during them)
+    if (k0 + kBK < K) load_tile<8>(tr, xrow, x_row_ok, w, wrow_off, w_row_ok, k0 + kBK, K, ak, wk, 0, w_vec);
+  }
+  csum[t] = colsum;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int cl = cg + 32 * j, col = n0 + cl;
+    if (col >= N) continue;
+    const int64_t s_n = int64_t(csum[2 * cl]) + int64_t(csum[2 * cl + 1]);
+    const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
+    const int sh = shifts ? int(shifts[col]) : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + rg + 8 * i;
+      if (row >= M) continue;
+      uint64_t v = corr;
+#pragma unroll
+      for (int dg = 0; dg < 8; ++dg) v += uint64_t(int64_t(acc[i][j][dg])) << (8 * dg);
+      v = sh < 64 ? (v << sh) : 0;
+      y[size_t(row) * N + col] = v & mask;
+    }
+  }
+}
+
+hipError_t launch_share_gemm_valu(const uint64_t* x, const int8_t* w, const int8_t* shifts, uint64_t* y, int M,
+                                  int K, int N, int mask_bits, hipStream_t s) {
+  const uint64_t mask = mask_bits >= 64 ? ~0ull : ((1ull << mask_bits) - 1);
+  const int w_vec = (K % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+  const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM);
+  hipLaunchKernelGGL(share_gemm_valu_kernel, grid, dim3(kThreads), 0, s, x, w, shifts, y, M, K, N, mask, w_vec);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- DMA path
 // For K % 64 == 0 and int8 weights (16-byte aligned x, w): the raw tiles go
 // from global memory straight into a two-stage LDS ring with
@@ -328,10 +432,16 @@ __device__ __forceinline__ void dma_step(const DmaCtx& c, bool next, int k_next,
   }
 }
 
+// Weight planes: w holds `planes` int8 matrices [planes][N][K], plane e the
+// signed byte of weight digit e (planes = 1: int8 weights; 3: the pre-split
+// f12 weights).  Workgroup z takes plane z / splits and K split z % splits;
+// plane e's products enter y shifted by 8e.
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
     share_gemm_dma_kernel(const uint64_t* __restrict__ x, const int8_t* __restrict__ w,
                           const int8_t* __restrict__ shifts, uint64_t* __restrict__ y, int M, int K, int N,
-                          uint64_t mask, int k_split) {
+                          uint64_t mask, int k_split, int splits) {
+  const int plane = int(blockIdx.z) / splits, split_z = int(blockIdx.z) % splits;
+  w += size_t(plane) * size_t(N) * size_t(K);
   __shared__ __attribute__((aligned(16))) uint8_t raw0[kBM * kRawRow];
   __shared__ __attribute__((aligned(16))) uint8_t raw1[kBM * kRawRow];
   __shared__ __attribute__((aligned(16))) uint8_t wt0[kBN * kBK];
@@ -378,7 +488,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   // split-K: workgroup z takes K steps [z k_split, (z+1) k_split); with more
   // than one split the partial products are added into y (zeroed first) by
   // 64-bit atomics, exact mod 2^64 in any order
-  const int k_begin = int(blockIdx.z) * k_split;
+  const int k_begin = split_z * k_split;
   const int steps = min(k_split, K - k_begin) / kBK;
   dma_issue(c, k_begin, raw0, wt0);
   for (int s = 0; s < steps; s += 2) {
@@ -399,7 +509,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     if (col >= N) continue;
     const int64_t s_n = int64_t(csum[2 * c2]) + int64_t(csum[2 * c2 + 1]);
     const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
-    const int sh = shifts ? int(shifts[col]) : 0;
+    const int sh = 8 * plane + (shifts ? int(shifts[col]) : 0);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
@@ -425,13 +535,32 @@ __global__ void __launch_bounds__(256) gemm_clear_kernel(uint64_t* __restrict__ 
     y[i] = keep ? (y[i] & keep) : 0;
 }
 
+// Pre-split weights: planes[e][i] = balanced signed byte e of w[i] (w in
+// [-0x808080, 0x7F7F7F]), so that w = sum_e planes[e] 256^e.
+__global__ void __launch_bounds__(256) weight_split_kernel(const int32_t* __restrict__ w, int8_t* __restrict__ planes,
+                                                           size_t count) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += size_t(gridDim.x) * blockDim.x) {
+    const int v = w[i];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) planes[size_t(e) * count + i] = int8_t(weight_digit(v, e));
+  }
+}
+
+hipError_t launch_weight_split(const int32_t* w, int8_t* planes, size_t count, hipStream_t s) {
+  if (!count) return hipSuccess;
+  const unsigned grid = unsigned(std::min<size_t>((count + 255) / 256, 8192));
+  hipLaunchKernelGGL(weight_split_kernel, dim3(grid), dim3(256), 0, s, w, planes, count);
+  return hipGetLastError();
+}
+
 hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
                              int M, int K, int N, int mask_bits, hipStream_t s) {
   const uint64_t mask = mask_bits >= 64 ? ~0ull : ((1ull << mask_bits) - 1);
   const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(kThreads);
   // 16-byte weight loads need 16-byte aligned rows
   const int w_vec = (K % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
-  if (w_bits == 8) {
+  if (w_bits == 8 || w_bits == 24) {
+    const int planes = w_bits == 8 ? 1 : 3;
     if (K % kBK == 0 && w_vec && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
       // Split K while the tiles fill fewer than 256 workgroups (one per CU;
       // N = 1024 at M = 512 gives 128 tiles) and each split keeps >= 8 steps:
@@ -444,22 +573,32 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
       splits = (K + k_split - 1) / k_split;
       const size_t words = size_t(M) * N;
       const unsigned fgrid = unsigned(std::min<size_t>((words + 255) / 256, 4096));
-      if (splits > 1) {
+      // several planes or K splits add their partial products into y
+      const bool atomic = splits * planes > 1;
+      if (atomic) {
         hipLaunchKernelGGL(gemm_clear_kernel, dim3(fgrid), dim3(256), 0, s, y, words, 0ull);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
       }
-      hipLaunchKernelGGL(share_gemm_dma_kernel, dim3(grid.x, grid.y, unsigned(splits)), block, 0, s, x,
-                         static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split);
+      hipLaunchKernelGGL(share_gemm_dma_kernel, dim3(grid.x, grid.y, unsigned(splits * planes)), block, 0, s, x,
+                         static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split, splits);
       hipError_t e = hipGetLastError();
-      if (e == hipSuccess && splits > 1 && mask != ~0ull) {
+      if (e == hipSuccess && atomic && mask != ~0ull) {
         hipLaunchKernelGGL(gemm_clear_kernel, dim3(fgrid), dim3(256), 0, s, y, words, mask);
         e = hipGetLastError();
       }
       return e;
     }
-    hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, 0, 0, w_vec);
-    return hipGetLastError();
+    // register-staged kernel, one launch per plane (plane e shifted by 8e,
+    // accumulated into y after the first)
+    for (int e = 0; e < planes; ++e) {
+      const int8_t* we = static_cast<const int8_t*>(w) + size_t(e) * size_t(N) * size_t(K);
+      hipLaunchKernelGGL((share_gemm_kernel<8>), grid, block, 0, s, x, we, shifts, y, M, K, N, mask, e, e > 0,
+                         w_vec);
+      const hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
   }
   for (int e = 0; e < 3; ++e) {
     hipLaunchKernelGGL((share_gemm_kernel<32>), grid, block, 0, s, x, w, shifts, y, M, K, N, mask, e, e > 0, 0);

@@ -165,6 +165,33 @@ int praghip_weights_upload(const praghip_weights* w, int device, int32_t* dst, v
   return PRAGHIP_OK;
 }
 
+// Host split into the three balanced signed bytes (w = sum_e b_e 256^e with
+// b_e in [-128, 127]) of praghip_share_gemm's w_bits 24, then one copy.
+int praghip_weights_upload_split(const praghip_weights* w, int device, int8_t* dst, void* stream) {
+  if (!w || !dst) return set_error(PRAGHIP_E_ARGUMENT, "E_NULL");
+  const size_t count = w->rows * w->cols;
+  const int32_t* src = w->data();
+  std::vector<int8_t> planes(3 * count);
+  for (size_t i = 0; i < count; ++i) {
+    int v = src[i];
+    if (v < -0x808080 || v > 0x7F7F7F) return set_error(PRAGHIP_E_SHAPE, "E_WEIGHT_RANGE");
+    for (int e = 0; e < 3; ++e) {
+      const int8_t b = int8_t(v & 0xff);  // the low byte as a signed value
+      planes[size_t(e) * count + i] = b;
+      v = (v - b) >> 8;
+    }
+  }
+  int previous = 0;
+  hipError_t e = hipGetDevice(&previous);
+  if (e == hipSuccess && previous != device) e = hipSetDevice(device);
+  const auto s = static_cast<hipStream_t>(stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(dst, planes.data(), planes.size(), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (previous != device) (void)hipSetDevice(previous);
+  if (e != hipSuccess) return set_error(PRAGHIP_E_DEVICE, std::string("E_WEIGHT_HIP: ") + hipGetErrorString(e));
+  return PRAGHIP_OK;
+}
+
 void praghip_weights_close(praghip_weights* w) { delete w; }
 
 }  // extern "C"

@@ -26,7 +26,8 @@ from ._lib import Cleanup, PraghipError, Timing, check, lib  # noqa: F401
 from .ntt import NttBatch, ntt_tables  # noqa: F401
 from .keyswitch import Switch  # noqa: F401
 from .shares import (LocalShares, ShareStorage, bfv_delta, dyadic_mac, lift59, local_dot_scale,  # noqa: F401
-                     local_dot_scale_noalloc, ring_add, ring_layout, ring_scale, ring_sum_rows, share_gemm)
+                     local_dot_scale_noalloc, ring_add, ring_layout, ring_scale, ring_sum_rows, share_gemm,
+                     share_gemm_valu, split_weights)
 from .weights import MappedWeights  # noqa: F401
 from .qwen3 import QWEN3_0_6B, Qwen3LocalGemms, Qwen3Shape  # noqa: F401
 from .matrix import Matrix, MatrixPacking, PublicZero, matrix_packing  # noqa: F401

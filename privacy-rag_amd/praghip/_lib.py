@@ -80,6 +80,8 @@ SIGNATURES = {
     "praghip_switch_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_switch_destroy": (None, [vp]),
     "praghip_share_gemm": (i32, [i32, vp, vp, i32, vp, vp, sz, sz, sz, i32, vp]),
+    "praghip_share_gemm_valu": (i32, [i32, vp, vp, vp, vp, sz, sz, sz, i32, vp]),
+    "praghip_weights_split": (i32, [i32, vp, vp, sz, vp]),
     "praghip_ring_add": (i32, [i32, vp, vp, vp, sz, i32, vp]),
     "praghip_ring_scale": (i32, [i32, vp, u64, vp, sz, i32, vp]),
     "praghip_ring_layout": (i32, [i32, vp, sz, vp, vp, sz, vp]),
@@ -144,6 +146,7 @@ SIGNATURES = {
     "praghip_weights_at": (i32, [vp, sz, sz, ctypes.POINTER(u64)]),
     "praghip_weights_max_abs": (i32, [vp, ctypes.POINTER(u64)]),
     "praghip_weights_upload": (i32, [vp, i32, vp, vp]),
+    "praghip_weights_upload_split": (i32, [vp, i32, vp, vp]),
     "praghip_weights_close": (None, [vp]),
     "praghip_frame_encode": (i32, [ctypes.POINTER(FrameHeaderT), vp]),
     "praghip_frame_decode": (i32, [vp, ctypes.POINTER(FrameHeaderT)]),

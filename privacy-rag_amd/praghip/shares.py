@@ -12,20 +12,29 @@ def share_gemm(x, w, y=None, shifts=None, mask_bits: int = 64, stream=None):
 
     x: GPU u64 [M][K] shares; w: GPU int8 or int32 [N][K] (the reference's
     [out][in] order; int32 values must lie in [-0x808080, 0x7F7F7F], which holds
-    the reference f12 domain |w| <= 2^20); shifts: GPU int8 [N] or None.
-    The loop of bfv_matrix.inc:101-105 with mask_bits=59 is the reference ring.
+    the reference f12 domain |w| <= 2^20), or int8 [3][N][K]: such int32
+    weights pre-split into signed-byte planes (split_weights,
+    MappedWeights.upload_split), the fast form of static weights; shifts:
+    GPU int8 [N] or None.  The loop of bfv_matrix.inc:101-105 with
+    mask_bits=59 is the reference ring.
     """
     import torch
     m, k = x.shape
-    n, k2 = w.shape
+    if w.dim() == 3:
+        if w.dtype != torch.int8 or w.shape[0] != 3:
+            raise TypeError("pre-split weights must be int8 [3][N][K]")
+        n, k2 = w.shape[1:]
+        w_bits = 24
+    else:
+        n, k2 = w.shape
+        if w.dtype == torch.int8:
+            w_bits = 8
+        elif w.dtype == torch.int32:
+            w_bits = 32
+        else:
+            raise TypeError("weights must be int8 or int32")
     if k != k2:
         raise ValueError("inner dimensions differ")
-    if w.dtype == torch.int8:
-        w_bits = 8
-    elif w.dtype == torch.int32:
-        w_bits = 32
-    else:
-        raise TypeError("weights must be int8 or int32")
     if y is None:
         y = torch.empty((m, n), dtype=torch.int64, device=x.device)
     if tuple(y.shape) != (m, n) or (shifts is not None and shifts.numel() != n):
@@ -37,6 +46,38 @@ def share_gemm(x, w, y=None, shifts=None, mask_bits: int = 64, stream=None):
     check(lib().praghip_share_gemm(x.device.index or 0, dev_ptr(x, u64_dtypes()), dev_ptr(w), w_bits, sp,
                                    dev_ptr(y, u64_dtypes()), m, k, n, mask_bits, stream_handle(stream)))
     return y
+
+
+def share_gemm_valu(x, w, y=None, shifts=None, mask_bits: int = 64, stream=None):
+    """share_gemm with int8 weights on VALU dot products instead of the matrix
+    cores (the measured alternative to the MFMA kernels); same results."""
+    import torch
+    m, k = x.shape
+    n, k2 = w.shape
+    if k != k2 or w.dtype != torch.int8:
+        raise ValueError("int8 weights [N][K] expected")
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.int64, device=x.device)
+    sp = None if shifts is None else dev_ptr(shifts, (torch.int8,))
+    check(lib().praghip_share_gemm_valu(x.device.index or 0, dev_ptr(x, u64_dtypes()), dev_ptr(w), sp,
+                                        dev_ptr(y, u64_dtypes()), m, k, n, mask_bits, stream_handle(stream)))
+    return y
+
+
+def split_weights(w, out=None, stream=None):
+    """int32 [N][K] weights in [-0x808080, 0x7F7F7F] on the GPU -> int8
+    [3][N][K] signed-byte planes (w = sum_e plane_e 256^e), the w_bits 24
+    form of share_gemm."""
+    import torch
+    if w.dtype != torch.int32 or w.dim() != 2:
+        raise TypeError("weights must be int32 [N][K]")
+    n, k = w.shape
+    if out is None:
+        out = torch.empty((3, n, k), dtype=torch.int8, device=w.device)
+    if tuple(out.shape) != (3, n, k) or out.dtype != torch.int8:
+        raise shape_error("E_SHARE_SHAPE")
+    check(lib().praghip_weights_split(w.device.index or 0, dev_ptr(w), dev_ptr(out), n * k, stream_handle(stream)))
+    return out
 
 
 RING_BITS = 59

@@ -54,6 +54,18 @@ class MappedWeights:
         check(lib().praghip_weights_upload(self._handle(), dst.device.index or 0, dev_ptr(dst), s))
         return dst
 
+    def upload_split(self, dst, stream=None):
+        """Split on the host into the three signed-byte planes and copy into a GPU
+        int8 tensor [3][rows][cols] (share_gemm's pre-split form, w_bits 24)."""
+        import torch
+        if dst.dtype != torch.int8 or dst.numel() != 3 * self.rows * self.cols:
+            raise ValueError("E_NPY_SHAPE")
+        s = None if stream is None else ctypes.c_void_p(stream.cuda_stream).value
+        if s is None:
+            s = ctypes.c_void_p(torch.cuda.current_stream(dst.device).cuda_stream).value
+        check(lib().praghip_weights_upload_split(self._handle(), dst.device.index or 0, dev_ptr(dst), s))
+        return dst
+
     def close(self):
         if self._h is not None:
             lib().praghip_weights_close(self._h)

@@ -11,10 +11,13 @@ from conftest import from_dev, to_dev
 pytestmark = pytest.mark.gpu
 
 
-def _run(x, w, shifts=None, mask_bits=64):
+def _run(x, w, shifts=None, mask_bits=64, split=False):
+    """split: int32 weights pre-split on the GPU into three signed-byte planes (w_bits 24)."""
     import torch
     tx = to_dev(x)
     tw = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+    if split:
+        tw = praghip.split_weights(tw)
     ts = None if shifts is None else torch.from_numpy(np.ascontiguousarray(shifts, dtype=np.int8)).cuda()
     y = praghip.share_gemm(tx, tw, shifts=ts, mask_bits=mask_bits)
     torch.cuda.synchronize()
@@ -34,7 +37,7 @@ def test_gemm_golden(gpu, golden_dir):
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (5, 7, 3), (33, 65, 129), (64, 128, 256), (100, 1000, 300),
                                    (31, 2048, 127), (512, 64, 128)])
-@pytest.mark.parametrize("wdt", ["i8", "i32"])
+@pytest.mark.parametrize("wdt", ["i8", "i32", "i32split"])
 def test_gemm_ragged_vs_oracle(gpu, m, k, n, wdt):
     print(f"[gemm] m={m} k={k} n={n} {wdt}", flush=True)
     x = oracle.fill_u64(m * k, 1000 + m).reshape(m, k)
@@ -46,7 +49,7 @@ def test_gemm_ragged_vs_oracle(gpu, m, k, n, wdt):
     sh = oracle.fill_shift(n, 4000 + k)
     for shifts, mask in ((None, 64), (sh, 59)):
         want = oracle.share_gemm(x, w, shifts, mask)
-        np.testing.assert_array_equal(_run(x, w, shifts, mask), want)
+        np.testing.assert_array_equal(_run(x, w, shifts, mask, split=wdt == "i32split"), want)
 
 
 def test_gemm_extreme_values(gpu):
@@ -65,6 +68,7 @@ def test_gemm_extreme_values(gpu):
     w32[2] = 0x7F7F7F  # largest weight with three balanced signed bytes
     w32[3] = -0x808080  # smallest
     np.testing.assert_array_equal(_run(x, w32), oracle.share_gemm(x, w32))
+    np.testing.assert_array_equal(_run(x, w32, split=True), oracle.share_gemm(x, w32))
 
 
 def test_gemm_c4_full_shape(gpu):
@@ -86,3 +90,47 @@ def test_gemm_split_k_shapes(gpu, m, k, n):
     sh = oracle.fill_shift(n, 7000 + k)
     for shifts, mask in ((None, 64), (sh, 59)):
         np.testing.assert_array_equal(_run(x, w, shifts, mask), oracle.share_gemm(x, w, shifts, mask))
+
+
+def test_gemm_c4_f12_presplit(gpu, tmp_path):
+    """C4's shape with the reference's weight domain (int32 f12, |w| <= 2^20,
+    quantize_weights.py:91,102) pre-split into three signed-byte planes: once
+    on the GPU (split_weights) and once on the host at upload
+    (MappedWeights.upload_split), both identical and bit-exact against the
+    oracle's int32 product, shifts and the 59-bit ring included."""
+    import torch
+    m, k, n = 512, 1024, 3072
+    x = oracle.fill_u64(m * k, 0x5052414700000014).reshape(m, k)
+    w = ((oracle.fill_u64(n * k, 0x5052414700000114) % np.uint64((1 << 21) + 1)).astype(np.int64)
+         - (1 << 20)).astype("<i4").reshape(n, k)
+    w[0, :4] = [1 << 20, -(1 << 20), 0x7F7F7F, -0x808080]
+    sh = oracle.fill_shift(n, 0x5052414700000214)
+    planes = praghip.split_weights(torch.from_numpy(w).cuda())
+    path = tmp_path / "model.layers.0.mlp.up_proj.weight.npy"
+    np.save(path, w)
+    host_planes = torch.empty((3, n, k), dtype=torch.int8, device="cuda")
+    with praghip.MappedWeights(str(path), n, k) as mw:
+        mw.upload_split(host_planes)
+    torch.cuda.synchronize()
+    assert torch.equal(planes, host_planes)
+    tx, ts = to_dev(x), torch.from_numpy(sh).cuda()
+    for shifts, mask in ((None, 64), (ts, 59)):
+        y = praghip.share_gemm(tx, planes, shifts=shifts, mask_bits=mask)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_dev(y), oracle.share_gemm(x, w, None if shifts is None else sh, mask))
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 1024, 3072), (33, 100, 129), (1, 64, 1)])
+def test_gemm_valu_form(gpu, m, k, n):
+    """The VALU dot-product form (the measured alternative to the MFMA
+    kernels) gives the oracle's results, shifts and the 59-bit ring included."""
+    import torch
+    print(f"[gemm-valu] m={m} k={k} n={n}", flush=True)
+    x = oracle.fill_u64(m * k, 8000 + k).reshape(m, k)
+    w = oracle.fill_i8(n * k, 8100 + n).reshape(n, k)
+    sh = oracle.fill_shift(n, 8200 + m)
+    for shifts, mask in ((None, 64), (sh, 59)):
+        ts = None if shifts is None else torch.from_numpy(shifts).cuda()
+        y = praghip.share_gemm_valu(to_dev(x), torch.from_numpy(w).cuda(), shifts=ts, mask_bits=mask)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_dev(y), oracle.share_gemm(x, w, shifts, mask))

@@ -64,3 +64,14 @@ def test_format_errors(tmp_path, case):
         path, rows, code = _save(tmp_path, "a.npy", w), 0, "BAD_SHAPE"
     with pytest.raises(PraghipError, match=code):
         praghip.MappedWeights(path, rows, cols)
+
+
+def test_upload_split_rejects_out_of_range(tmp_path):
+    """The host split of praghip_weights_upload_split refuses a weight outside
+    the three-signed-byte range before any device call."""
+    from praghip import _lib
+    w = np.zeros((4, 8), dtype="<i4")
+    w[2, 3] = 0x7F7F7F + 1
+    with praghip.MappedWeights(_save(tmp_path, "big.npy", w), 4, 8) as m:
+        rc = _lib.lib().praghip_weights_upload_split(m._handle(), 0, 1 << 20, None)
+        assert rc == _lib.E_SHAPE and _lib.lib().praghip_last_error() == b"E_WEIGHT_RANGE"
