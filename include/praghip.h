@@ -74,6 +74,24 @@ int praghip_version(void);
  * when the runtime reports no device). */
 int praghip_device_count(void);
 
+/* Device binding (the UUID + PCI-bus binding of ntt.cu:86-90, which reads
+ * PRAG_ENC0_GPU_UUID / PRAG_ENC0_GPU_PCI; bfv_matrix.inc:35 and
+ * silu_gpu_bridge.cpp:27 read the same pair under other names).
+ * praghip_device_identity writes the two strings a binding compares:
+ * uuid "GPU-" + the 16 bytes of hipDeviceProp_t.uuid (as characters when all
+ * 16 are hex digits, the form rocminfo prints; else as 32 hex digits grouped
+ * 8-4-4-4-12), pci the hipDeviceGetPCIBusId string ("0000:c1:00.0").
+ * uuid_size >= 40, pci_size >= 16.  praghip_device_bind returns in *device
+ * the gfx950 device whose identity equals both (hex digits compared
+ * case-insensitively); praghip_device_bind_env reads the two values from the
+ * named environment variables (NULL names: PRAG_ENC0_GPU_UUID and
+ * PRAG_ENC0_GPU_PCI).  Errors: a variable unset or empty -> PRAGHIP_E_DEVICE
+ * "E_PHASE_DEVICE_BINDING"; no gfx950 device matches -> PRAGHIP_E_DEVICE
+ * "E_GFX950_REQUIRED" (the reference's E_RTX2060_REQUIRED). */
+int praghip_device_identity(int device, char *uuid, size_t uuid_size, char *pci, size_t pci_size);
+int praghip_device_bind(const char *uuid, const char *pci, int *device);
+int praghip_device_bind_env(const char *uuid_var, const char *pci_var, int *device);
+
 /* ---------------------------------------------------------------- tables */
 /* SEAL NTTTables for one prime q == 1 mod 2N, q < 2^62 (the arrays
  * seal_tables.cpp:22-33 extracts): fwd_pairs/inv_pairs [N][2], invn_pair [2].

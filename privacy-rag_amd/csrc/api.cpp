@@ -9,6 +9,7 @@
 // freed bytes, closed} from an idempotent close().
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -321,6 +322,92 @@ int praghip_device_count(void) {
     if (hipGetDeviceProperties(&prop, i) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ++good;
   }
   return good;
+}
+
+}  // extern "C"
+
+namespace {
+
+bool is_hex_digit(char c) {
+  return (c >= '0' && c <= '9') || (c >= 'a' && c <= 'f') || (c >= 'A' && c <= 'F');
+}
+
+// The binding strings of one device (empty on any runtime error).
+bool device_identity(int device, std::string& uuid, std::string& pci) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
+  const char* b = prop.uuid.bytes;
+  bool text = true;
+  for (int i = 0; i < 16; ++i) text = text && is_hex_digit(b[i]);
+  uuid = "GPU-";
+  if (text) {
+    uuid.append(b, 16);
+  } else {
+    static const char digits[] = "0123456789abcdef";
+    for (int i = 0; i < 16; ++i) {
+      if (i == 4 || i == 6 || i == 8 || i == 10) uuid += '-';
+      const unsigned v = static_cast<unsigned char>(b[i]);
+      uuid += digits[v >> 4];
+      uuid += digits[v & 15];
+    }
+  }
+  char bus[64] = {0};
+  if (hipDeviceGetPCIBusId(bus, sizeof(bus) - 1, device) != hipSuccess) return false;
+  pci = bus;
+  return true;
+}
+
+bool same_id(const std::string& a, const char* b) {
+  if (a.size() != std::strlen(b)) return false;
+  for (size_t i = 0; i < a.size(); ++i) {
+    char x = a[i], y = b[i];
+    if (x >= 'A' && x <= 'F') x = char(x - 'A' + 'a');
+    if (y >= 'A' && y <= 'F') y = char(y - 'A' + 'a');
+    if (x != y) return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int praghip_device_identity(int device, char* uuid, size_t uuid_size, char* pci, size_t pci_size) {
+  if (!uuid || !pci) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  if (uuid_size < 40 || pci_size < 16) return fail(PRAGHIP_E_ARGUMENT, "E_IDENTITY_BUFFER");
+  uuid[0] = pci[0] = 0;
+  if (int rc = check_device(device)) return rc;
+  std::string u, p;
+  if (!device_identity(device, u, p) || p.size() >= pci_size) return fail(PRAGHIP_E_DEVICE, "E_DEVICE_PROPERTIES");
+  std::memcpy(uuid, u.c_str(), u.size() + 1);
+  std::memcpy(pci, p.c_str(), p.size() + 1);
+  return PRAGHIP_OK;
+}
+
+int praghip_device_bind(const char* uuid, const char* pci, int* device) {
+  if (!device) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *device = -1;
+  if (!uuid || !pci || !*uuid || !*pci) return fail(PRAGHIP_E_DEVICE, "E_PHASE_DEVICE_BINDING");
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) count = 0;
+  for (int i = 0; i < count; ++i) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, i) != hipSuccess || std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) continue;
+    std::string u, p;
+    if (device_identity(i, u, p) && same_id(u, uuid) && same_id(p, pci)) {
+      *device = i;
+      return PRAGHIP_OK;
+    }
+  }
+  return fail(PRAGHIP_E_DEVICE, "E_GFX950_REQUIRED: no gfx950 device with this UUID and PCI bus id");
+}
+
+int praghip_device_bind_env(const char* uuid_var, const char* pci_var, int* device) {
+  if (!device) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *device = -1;
+  const char* uuid = std::getenv(uuid_var ? uuid_var : "PRAG_ENC0_GPU_UUID");
+  const char* pci = std::getenv(pci_var ? pci_var : "PRAG_ENC0_GPU_PCI");
+  return praghip_device_bind(uuid, pci, device);
 }
 
 int praghip_ntt_tables(uint64_t q, uint32_t log_n, uint64_t* fwd_pairs, uint64_t* inv_pairs, uint64_t* invn_pair,

@@ -22,6 +22,8 @@ libpraghip.so:
 Device data is handed over as torch tensors on the GPU (int64 or uint64 with
 u64 bit patterns); torch is used only for memory and streams.
 """
+from __future__ import annotations
+
 from ._lib import Cleanup, PraghipError, Timing, check, lib  # noqa: F401
 from .ntt import NttBatch, ntt_tables  # noqa: F401
 from .keyswitch import Switch  # noqa: F401
@@ -37,3 +39,28 @@ from . import frames, synth  # noqa: F401
 
 def device_count() -> int:
     return int(lib().praghip_device_count())
+
+
+def device_identity(device: int = 0) -> tuple[str, str]:
+    """(uuid, pci) of a gfx950 device: the two strings a binding compares
+    ("GPU-..." from hipDeviceProp_t.uuid, the PCI bus id)."""
+    import ctypes
+    uuid, pci = ctypes.create_string_buffer(64), ctypes.create_string_buffer(64)
+    check(lib().praghip_device_identity(int(device), uuid, 64, pci, 64))
+    return uuid.value.decode(), pci.value.decode()
+
+
+def bind_device(uuid: str | None = None, pci: str | None = None, *, uuid_var: str = "PRAG_ENC0_GPU_UUID",
+                pci_var: str = "PRAG_ENC0_GPU_PCI") -> int:
+    """Index of the gfx950 device with this UUID and PCI bus id (ntt.cu:86-90).
+    With uuid and pci both None the pair is read from the environment variables
+    `uuid_var` / `pci_var`; an unset variable raises E_PHASE_DEVICE_BINDING and
+    no matching device E_GFX950_REQUIRED."""
+    import ctypes
+    out = ctypes.c_int(-1)
+    if uuid is None and pci is None:
+        check(lib().praghip_device_bind_env(uuid_var.encode(), pci_var.encode(), ctypes.byref(out)))
+    else:
+        check(lib().praghip_device_bind(None if uuid is None else uuid.encode(),
+                                        None if pci is None else pci.encode(), ctypes.byref(out)))
+    return out.value

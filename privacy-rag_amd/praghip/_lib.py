@@ -60,6 +60,9 @@ SIGNATURES = {
     "praghip_last_error": (ctypes.c_char_p, []),
     "praghip_version": (i32, []),
     "praghip_device_count": (i32, []),
+    "praghip_device_identity": (i32, [i32, ctypes.c_char_p, sz, ctypes.c_char_p, sz]),
+    "praghip_device_bind": (i32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]),
+    "praghip_device_bind_env": (i32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]),
     "praghip_ntt_tables": (i32, [u64, u32, vp, vp, vp, vp]),
     "praghip_ntt_plan_create": (i32, [i32, vp, sz, u32, vp, vp, vp, sz, pp]),
     "praghip_ntt_forward": (i32, [vp, vp, sz, vp]),

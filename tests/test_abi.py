@@ -90,6 +90,40 @@ def test_no_device_here_is_reported():
     assert e.value.code == _lib.E_DEVICE and "E_GFX950_REQUIRED" in e.value.text
 
 
+def test_device_binding_requires_both_variables(monkeypatch):
+    """The UUID + PCI binding of ntt.cu:86-90: an unset or empty variable is
+    E_PHASE_DEVICE_BINDING before any device is looked at."""
+    monkeypatch.delenv("PRAG_ENC0_GPU_UUID", raising=False)
+    monkeypatch.setenv("PRAG_ENC0_GPU_PCI", "0000:c1:00.0")
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.bind_device()
+    assert e.value.code == _lib.E_DEVICE and e.value.text == "E_PHASE_DEVICE_BINDING"
+    monkeypatch.setenv("PRAG_ENC0_GPU_UUID", "")
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.bind_device()
+    assert e.value.text == "E_PHASE_DEVICE_BINDING"
+    monkeypatch.setenv("PRAG_SILU_GPU_UUID", "GPU-0000000000000000")
+    monkeypatch.delenv("PRAG_SILU_GPU_PCI", raising=False)
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.bind_device(uuid_var="PRAG_SILU_GPU_UUID", pci_var="PRAG_SILU_GPU_PCI")
+    assert e.value.text == "E_PHASE_DEVICE_BINDING"
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.bind_device(uuid="GPU-0000000000000000", pci=None)
+    assert e.value.text == "E_PHASE_DEVICE_BINDING"
+
+
+def test_device_binding_without_a_match():
+    """No gfx950 device has this identity (none at all without a GPU):
+    E_GFX950_REQUIRED, and the index stays -1."""
+    import ctypes
+    out = ctypes.c_int(7)
+    rc = _lib.lib().praghip_device_bind(b"GPU-not-a-device", b"ffff:ff:1f.7", ctypes.byref(out))
+    assert rc == _lib.E_DEVICE and out.value == -1
+    assert _lib.lib().praghip_last_error().decode().startswith("E_GFX950_REQUIRED")
+    buf = ctypes.create_string_buffer(64)
+    assert _lib.lib().praghip_device_identity(0, buf, 39, buf, 64) == _lib.E_ARGUMENT
+
+
 def test_share_entry_points_validate_before_device():
     """The ring ops, lift, dyadic MAC, local dot and batched GEMM reject bad
     arguments before any device call (fake, aligned addresses are never touched)."""

@@ -164,3 +164,26 @@ def test_ntt_rejects_misaligned_device_buffer(gpu):
         plan.forward(buf[1:])  # 8-byte aligned view
     assert "E_NTT_ALIGNMENT" in e.value.text
     assert torch.count_nonzero(buf) == 0  # nothing was launched
+
+
+def test_device_binding_by_uuid_and_pci(gpu, monkeypatch):
+    """ntt.cu:86-90: the plan's device chosen by the UUID + PCI bus id pair
+    from the environment; the bound index runs a transform."""
+    uuid, pci = praghip.device_identity(0)
+    print(f"[bind] device 0 uuid={uuid} pci={pci}", flush=True)
+    assert uuid.startswith("GPU-") and len(uuid) > 4 and len(pci) >= 7
+    assert praghip.bind_device(uuid, pci) == 0
+    assert praghip.bind_device(uuid.upper(), pci.upper()) == 0
+    monkeypatch.setenv("PRAG_ENC0_GPU_UUID", uuid)
+    monkeypatch.setenv("PRAG_ENC0_GPU_PCI", pci)
+    device = praghip.bind_device()
+    assert device == 0
+    with pytest.raises(praghip.PraghipError) as e:
+        praghip.bind_device(uuid, "ffff:ff:1f.7")
+    assert e.value.text.startswith("E_GFX950_REQUIRED")
+    q = P16384_50[:1]
+    a = oracle.fill_residues(1, 1 << 10, q, 0x51)
+    plan = praghip.NttBatch(q, 10, device=device)
+    t = to_dev(a)
+    plan.forward(t)
+    np.testing.assert_array_equal(from_dev(t), oracle.ntt(a, oracle.Tables(q, 10)))
