@@ -330,19 +330,26 @@ hipError_t launch_share_gemm_valu(const uint64_t* x, const int8_t* w, const int8
 
 // ---------------------------------------------------------------- DMA path
 // For K % 64 == 0 and int8 weights (16-byte aligned x, w): the raw tiles go
-// from global memory straight into a two-stage LDS ring with
+// from global memory straight into a three-stage LDS ring with
 // global_load_lds_dwordx4 (no registers, no wait until the stage is used), so
-// the next K step's loads are in flight during the current step's MFMAs; two
-// workgroups per CU overlap each other's waits as well.  Per step each thread
-// turns 8 shares of the raw tile into the 8 digit planes (as above), and the
-// weight tile is read by the MFMAs in place.
+// the next two K steps' loads are in flight during the current step's MFMAs;
+// two workgroups per CU overlap each other's waits as well.  The MFMA share
+// operands are read from the raw u64 tile with ds_read_b64_tr_b8, which hands
+// every lane one byte position of eight words: with the eight words of a row
+// k..k+7 as the source, lane i of each 8-lane half of a 16-lane group receives
+// digit i of those eight shares (the byte transpose is done by the LDS read,
+// with no VALU shuffle, no digit-plane copy and no second barrier per step).
 //
-// LDS: raw shares [2][32 rows][512 B], weights [2][128 rows][64 B] with the
-// 16-byte chunk index of row r stored at chunk ^ (r & 3) (conflict-free
-// operand reads without padding, which DMA cannot insert), digit planes
-// [8][34][80 B]: two spare rows per plane make the plane stride 2720 bytes
-// instead of 2560 (a multiple of the bank span), so the MFMA operand reads of
-// one row across the 8 digits spread over the banks (measured 3-5% faster).
+// MFMA rows of one 32x32x32 product: lane l of the A operand is digit l % 8 of
+// share row (l % 32) / 8, so a lane's 16 accumulator registers hold, for its
+// column, digits 4(l/32)..4(l/32)+3 of four share rows; the two halves of the
+// wave add their digit sums with one cross-half exchange.
+//
+// LDS: raw shares [3][32 rows][512 B] with the 16-byte chunk c of row r at
+// chunk c ^ 4(r & 7) (each 8-word read of a row stays one 64-byte block, and
+// the four rows of one read land on distinct banks), weights [3][128 rows][64 B]
+// with chunk c of row r at c ^ wt_swizzle(r).  DMA writes 64 lanes x 16 bytes in
+// order, so each lane loads the global chunk that belongs at its LDS slot.
 constexpr int kRawRow = kBK * 8;  // bytes of one raw share row per step
 
 // 16 bytes per lane from global memory straight into LDS at M0 + lane * 16
@@ -354,171 +361,351 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
+// Byte offset of share word k of raw row r in a stage buffer.
+__device__ __forceinline__ int raw_offset(int r, int k) {
+  return r * kRawRow + ((((k >> 1) ^ (4 * (r & 7)))) << 4) + ((k & 1) << 3);
+}
+
+// Chunk swizzle of weight row r (64-byte rows, four 16-byte chunks): 16-byte
+// reads of 8 consecutive rows land on 8 distinct 16-byte bank slots of a
+// 128-byte bank line, and those of rows r, r + 4, r + 8, r + 12 on 4 distinct
+// slots of a 256-byte one (bits: 2 (r/4 % 2) + (r/2 % 2 ^ r/8 % 2)).
+__device__ __forceinline__ int wt_swizzle(int r) { return 2 * ((r >> 2) & 1) + (((r >> 1) ^ (r >> 3)) & 1); }
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+// Eight bytes of the LDS transpose read at byte offset `off` of `base`.
+__device__ __forceinline__ v2i tr8(const uint8_t* base, int off) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((v2i __attribute__((address_space(3)))*)(base + off));
+}
+
 // One K step of the DMA path on stage buffers (raw, wt); the next step's DMAs
 // go to (raw_n, wt_n).  Distinct __shared__ objects per stage let the
 // compiler see that this step's LDS reads do not depend on the DMAs just
 // issued into the other stage (it would otherwise wait for them).
 struct DmaCtx {
   const uint8_t* xsrc[4];
-  const int8_t* wsrc[2];
-  int wave, ar, ak, cl, ch, i, khalf, a_row_in_block, a_digit, wm, wn;
+  const int8_t* wsrc[3];
+  int wave, i, khalf, wm, wn, tr_row, tr_k;
+  // operand read offsets within a stage: share word run h (k + 8h) of row
+  // block 0 at K step 0 is a_off[h]; row block rb, K step ks adds
+  // 2048 rb + 256 (ks ^ (rb & 1)).  Weight chunk of K step ks for block 0 is
+  // w_off[ks]; block cb adds 2048 cb.  (raw_offset and wt_swizzle, with the
+  // lane-independent parts moved into immediates.)
+  int a_off[2], w_off[2];
 };
 
-template <class RAW, class WT>
+// CB 32-column blocks per wave: a workgroup tile is 32 share rows x 64 CB
+// columns (waves 2 x 2, each 16 rows x 32 CB columns).
+template <int CB, class RAW, class WT>
 __device__ __forceinline__ void dma_issue(const DmaCtx& c, int k0, RAW& raw, WT& wt) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) dma16(c.xsrc[j] + size_t(k0) * 8, &raw[(2 * (4 * c.wave + j)) * kRawRow]);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) dma16(c.wsrc[j] + k0, &wt[(16 * (2 * c.wave + j)) * kBK]);
+  for (int j = 0; j < CB; ++j) dma16(c.wsrc[j] + k0, &wt[(16 * (CB * c.wave + j)) * kBK]);
 }
 
-template <class RAW, class WT, class RAWN, class WTN>
-__device__ __forceinline__ void dma_step(const DmaCtx& c, bool next, int k_next, const RAW& raw, const WT& wt,
-                                         RAWN& raw_n, WTN& wt_n, uint8_t (&a_lds)[8][kBM + 2][kPitch], int& colsum,
-                                         v16i (&acc)[4][2]) {
-  // this wave's DMAs for this step are done (none other is in flight yet);
-  // after the barrier every wave's are, and the previous step's reads are over
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  if (next) dma_issue(c, k_next, raw_n, wt_n);
-  // ---- raw shares -> 8 offset-binary digit planes
-  {
-    const uint4* rp = reinterpret_cast<const uint4*>(&raw[c.ar * kRawRow + c.ak * 8]);
-    const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
-    uint32_t d[16] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
-#pragma unroll
-    for (int e = 0; e < 16; ++e) d[e] ^= 0x80808080u;
-    uint32_t o[4][4];
-    transpose4(d[0], d[2], d[4], d[6], o[0][0], o[0][1], o[0][2], o[0][3]);
-    transpose4(d[8], d[10], d[12], d[14], o[1][0], o[1][1], o[1][2], o[1][3]);
-    transpose4(d[1], d[3], d[5], d[7], o[2][0], o[2][1], o[2][2], o[2][3]);
-    transpose4(d[9], d[11], d[13], d[15], o[3][0], o[3][1], o[3][2], o[3][3]);
-#pragma unroll
-    for (int dg = 0; dg < 4; ++dg) {
-      *reinterpret_cast<uint2*>(&a_lds[dg][c.ar][c.ak]) = make_uint2(o[0][dg], o[1][dg]);
-      *reinterpret_cast<uint2*>(&a_lds[dg + 4][c.ar][c.ak]) = make_uint2(o[2][dg], o[3][dg]);
-    }
+// Three stages: step s computes on stage s % 3 while the DMAs of steps s + 1
+// (issued one step earlier) and s + 2 (issued here, into the stage step s - 1
+// read) are in flight.
+template <int CB, class RAW, class WT, class RAWN, class WTN>
+__device__ __forceinline__ void dma_step(const DmaCtx& c, bool ahead, bool next, int k_next, const RAW& raw,
+                                         const WT& wt, RAWN& raw_n, WTN& wt_n, int (&colsum)[CB],
+                                         v16i (&acc)[4][CB]) {
+  // this wave's DMAs for this step are done: loads complete in order, and
+  // `ahead` says whether the next step's 4 + CB are still allowed in flight;
+  // after the barrier every wave's are, and every wave has finished reading
+  // the stage the new DMAs overwrite
+  if (ahead) {
+    if (CB == 2)
+      asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(7)\n\ts_barrier" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   }
-  // ---- column sums of the weight tile
-  {
-    const uint8_t* wrow = &wt[c.cl * kBK];
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const uint4 v = *reinterpret_cast<const uint4*>(wrow + (((2 * c.ch + cc) ^ (c.cl & 3)) * 16));
-      colsum = __builtin_amdgcn_sdot4(int(v.x), 0x01010101, colsum, false);
-      colsum = __builtin_amdgcn_sdot4(int(v.y), 0x01010101, colsum, false);
-      colsum = __builtin_amdgcn_sdot4(int(v.z), 0x01010101, colsum, false);
-      colsum = __builtin_amdgcn_sdot4(int(v.w), 0x01010101, colsum, false);
-    }
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  // ---- MFMA over the two 32-wide K steps
+  if (next) dma_issue<CB>(c, k_next, raw_n, wt_n);
+  // ---- every operand of the step first (16 transpose reads, 2 CB weight
+  // reads), so that the MFMAs then issue back to back behind one LDS wait
+  v4i aop[kBK / 32][4], bop[kBK / 32][CB];
 #pragma unroll
   for (int ks = 0; ks < kBK / 32; ++ks) {
     const int chunk = ks * 2 + c.khalf;  // logical 16-byte chunk of the weight rows
-    v4i bop[2];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int row = c.wn * 64 + cb * 32 + c.i;
-      bop[cb] = *reinterpret_cast<const v4i*>(&wt[row * kBK + ((chunk ^ (row & 3)) * 16)]);
+    for (int cb = 0; cb < CB; ++cb) {
+      const int row = c.wn * 32 * CB + cb * 32 + c.i;
+      bop[ks][cb] = *reinterpret_cast<const v4i*>(&wt[row * kBK + ((chunk ^ wt_swizzle(row)) * 16)]);
     }
-    const int kb = ks * 32 + c.khalf * 16;
+    const int k = ks * 32 + c.tr_k;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      const v4i aop = *reinterpret_cast<const v4i*>(&a_lds[c.a_digit][c.wm * 16 + rb * 4 + c.a_row_in_block][kb]);
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-        acc[rb][cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop[cb], acc[rb][cb], 0, 0, 0);
+      const int r = c.wm * 16 + rb * 4 + c.tr_row;
+      const v2i lo = tr8(raw, raw_offset(r, k)), hi = tr8(raw, raw_offset(r, k + 8));
+      aop[ks][rb] = v4i{lo.x, lo.y, hi.x, hi.y};
     }
   }
+  // ---- MFMA over the two 32-wide K steps
+#pragma unroll
+  for (int ks = 0; ks < kBK / 32; ++ks) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      // offset-binary digits: a_d = b_d - 128
+      const v4i a = aop[ks][rb] ^ int(0x80808080u);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+        acc[rb][cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bop[ks][cb], acc[rb][cb], 0, 0, 0);
+    }
+  }
+  // ---- column sums from the weight operands already in registers (lanes l
+  // and l ^ 32 hold the two halves of each row's K chunk; VALU work beside
+  // the MFMAs)
+#pragma unroll
+  for (int ks = 0; ks < kBK / 32; ++ks)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) colsum[cb] = __builtin_amdgcn_sdot4(bop[ks][cb][e], 0x01010101, colsum[cb], false);
+}
+
+// Software-pipelined form (CB = 3, one wave per SIMD): each step runs as two
+// halves of one 32-wide K step each, and the operands of the next half are
+// read from LDS while the MFMAs of the current half run, so LDS reads and the
+// matrix cores overlap within the wave with two operand sets in registers.
+template <int CB>
+struct HalfOps {
+  v4i a[4], b[CB];
+};
+
+template <int CB, class RAW, class WT>
+__device__ __forceinline__ void read_half(const DmaCtx& c, int ks, const RAW& raw, const WT& wt, HalfOps<CB>& o) {
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) o.b[cb] = *reinterpret_cast<const v4i*>(&wt[c.w_off[ks] + 2048 * cb]);
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int blk = 2048 * rb + 256 * (ks ^ (rb & 1));
+    const v2i lo = tr8(raw, c.a_off[0] + blk), hi = tr8(raw, c.a_off[1] + blk);
+    o.a[rb] = v4i{lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
+template <int CB>
+__device__ __forceinline__ void mfma_half(HalfOps<CB>& o, int (&colsum)[CB], v16i (&acc)[4][CB]) {
+  // offset-binary digits, in place, all four before the first MFMA (a VALU
+  // write just before the MFMA that reads it stalls the issue)
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) o.a[rb] ^= int(0x80808080u);
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+      acc[rb][cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[rb], o.b[cb], acc[rb][cb], 0, 0, 0);
+  }
+  // column sums from the weight operands (lanes l and l ^ 32 hold the two
+  // halves of each row's K chunk)
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) colsum[cb] = __builtin_amdgcn_sdot4(o.b[cb][e], 0x01010101, colsum[cb], false);
+}
+
+// 3 + 8 LDS reads among the 4 CB MFMAs of a half.
+template <int CB>
+__device__ __forceinline__ void interleave_half() {
+  __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // the four digit XORs
+#pragma unroll
+  for (int j = 0; j < CB + 8; ++j) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+  }
+}
+
+// Step s: half A reads K step 1 of stage s (raw_s, wt_s) into h1 while the
+// MFMAs of K step 0 run from h0; then the wait for step s + 1's stage and the
+// refill of stage s with step s + 3 (past the last step: the last step's tile
+// again, never read); half B reads K step 0 of stage s + 1 (raw_n, wt_n; past
+// the last step: stale data, never used) into h0 while the MFMAs of K step 1
+// run from h1.
+template <int CB, class RAWS, class WTS, class RAWN, class WTN>
+__device__ __forceinline__ void piped_step(const DmaCtx& c, int s, int steps, int k_begin, RAWS raw_s, WTS wt_s,
+                                           RAWN raw_n, WTN wt_n, HalfOps<CB>& h0, HalfOps<CB>& h1,
+                                           int (&colsum)[CB], v16i (&acc)[4][CB]) {
+  read_half<CB>(c, 1, raw_s, wt_s, h1);
+  mfma_half<CB>(h0, colsum, acc);
+  interleave_half<CB>();
+  // step s + 1's DMAs are done when only step s + 2's (4 + CB = 7) remain in
+  // flight, and this wave's reads of stage s are done; after the barrier both
+  // hold for every wave, so stage s may be refilled
+  asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  dma_issue<CB>(c, k_begin + min(s + 3, steps - 1) * kBK, raw_s, wt_s);
+  read_half<CB>(c, 0, raw_n, wt_n, h0);
+  mfma_half<CB>(h1, colsum, acc);
+  interleave_half<CB>();
+}
+
+// The other half of the wave's value (lane l ^ 32), 64 bits.
+__device__ __forceinline__ uint64_t swap_halves(uint64_t v, int lane) {
+  const int addr = (lane ^ 32) << 2;
+  const uint32_t lo = uint32_t(__builtin_amdgcn_ds_bpermute(addr, int(uint32_t(v))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_ds_bpermute(addr, int(uint32_t(v >> 32))));
+  return uint64_t(lo) | (uint64_t(hi) << 32);
+}
+
+// Tile (tm, tn) of this workgroup in the gridDim.y x gridDim.x tile grid.
+// Workgroups go to the 8 XCDs round robin (linear id mod 8), so when the grid
+// holds a multiple of 8 tiles XCD x is given the contiguous range
+// [x nt/8, (x+1) nt/8) of a grouped order (8 tile rows at a time, column by
+// column within the group): a compact block of tiles whose share rows and
+// weight columns stay in that XCD's L2 (512 x 3072 in 32 x 192 tiles: each
+// XCD 8 x 4 tiles, 2 MiB of shares and 768 KiB of weights).  Any bijection
+// is correct; this one only places the reuse.
+__device__ __forceinline__ void tile_of(int& tm, int& tn) {
+  const int TN = int(gridDim.x), TM = int(gridDim.y), nt = TN * TM;
+  int t = int(blockIdx.y) * TN + int(blockIdx.x);
+  if (nt % 8 == 0) t = (t % 8) * (nt / 8) + t / 8;
+  constexpr int G = 8;
+  const int group = t / (G * TN), first = group * G, rows = min(G, TM - first);
+  const int in = t - group * G * TN;
+  tm = first + in % rows;
+  tn = in / rows;
 }
 
 // Weight planes: w holds `planes` int8 matrices [planes][N][K], plane e the
 // signed byte of weight digit e (planes = 1: int8 weights; 3: the pre-split
 // f12 weights).  Workgroup z takes plane z / splits and K split z % splits;
-// plane e's products enter y shifted by 8e.
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// plane e's products enter y shifted by 8e.  CB = 2: 128-column tiles, two
+// workgroups (two waves per SIMD) per CU, whose waits overlap; CB = 3:
+// 192-column tiles, one workgroup per CU, 12 accumulator tiles per wave, so
+// that every MFMA takes fewer operand bytes from L2 and LDS.
+template <int CB>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(CB == 2 ? 2 : 1, CB == 2 ? 2 : 1)))
     share_gemm_dma_kernel(const uint64_t* __restrict__ x, const int8_t* __restrict__ w,
                           const int8_t* __restrict__ shifts, uint64_t* __restrict__ y, int M, int K, int N,
                           uint64_t mask, int k_split, int splits) {
+  constexpr int BN = 64 * CB;
   const int plane = int(blockIdx.z) / splits, split_z = int(blockIdx.z) % splits;
   w += size_t(plane) * size_t(N) * size_t(K);
   __shared__ __attribute__((aligned(16))) uint8_t raw0[kBM * kRawRow];
   __shared__ __attribute__((aligned(16))) uint8_t raw1[kBM * kRawRow];
-  __shared__ __attribute__((aligned(16))) uint8_t wt0[kBN * kBK];
-  __shared__ __attribute__((aligned(16))) uint8_t wt1[kBN * kBK];
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[8][kBM + 2][kPitch];
-  __shared__ int csum[kThreads];
+  __shared__ __attribute__((aligned(16))) uint8_t raw2[kBM * kRawRow];
+  __shared__ __attribute__((aligned(16))) uint8_t wt0[BN * kBK];
+  __shared__ __attribute__((aligned(16))) uint8_t wt1[BN * kBK];
+  __shared__ __attribute__((aligned(16))) uint8_t wt2[BN * kBK];
 
   const int t = threadIdx.x, lane = t & 63;
   DmaCtx c;
   c.wave = t >> 6;
   c.wm = c.wave >> 1;
   c.wn = c.wave & 1;
-  c.ar = t >> 3;  // transposer: raw row ar, shares ak..ak+7
-  c.ak = (t & 7) * 8;
-  c.cl = t >> 1;  // column sum: weight row cl, half ch
-  c.ch = t & 1;
   c.i = lane & 31;
   c.khalf = lane >> 5;
-  c.a_row_in_block = 2 * ((c.i >> 2) & 1) + (c.i >> 4);
-  c.a_digit = 4 * ((c.i >> 3) & 1) + (c.i & 3);
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  // transpose-read source of this lane: share row 2((l/16) % 2) + l % 2 of
+  // the 4-row block, word (l/2) % 8 of the 8-word run at k = 16(l/32)
+  c.tr_row = 2 * ((lane >> 4) & 1) + (lane & 1);
+  c.tr_k = 16 * (lane >> 5) + ((lane >> 1) & 7);
+  {
+    const int j = (lane >> 1) & 7;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      c.a_off[h] = (c.wm * 16 + c.tr_row) * kRawRow + 16 * (((8 * c.khalf + 4 * h) ^ (4 * c.tr_row)) + (j >> 1)) +
+                   8 * (j & 1);
+    const int f = wt_swizzle(c.i);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      c.w_off[ks] = (c.wn * 32 * CB + c.i) * kBK + 16 * (2 * (ks ^ (f >> 1)) + (c.khalf ^ (f & 1)));
+  }
+  int tm, tn;
+  tile_of(tm, tn);
+  const int m0 = tm * kBM, n0 = tn * BN;
   // DMA sources of this lane: 4 raw-share instructions (2 rows of 512 B each)
-  // and 2 weight instructions (16 rows of 64 B each) per wave and step.
+  // and CB weight instructions (16 rows of 64 B each) per wave and step.
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = 2 * (4 * c.wave + j) + (lane >> 5);
     const int grow = min(m0 + row, M - 1);  // rows past M: any valid row, results dropped
-    c.xsrc[j] = reinterpret_cast<const uint8_t*>(x + size_t(grow) * K) + (lane & 31) * 16;
+    const int ck = (lane & 31) ^ (4 * (row & 7));  // logical chunk stored at physical chunk lane & 31
+    c.xsrc[j] = reinterpret_cast<const uint8_t*>(x + size_t(grow) * K) + ck * 16;
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = 16 * (2 * c.wave + j) + (lane >> 2);
+  for (int j = 0; j < CB; ++j) {
+    const int row = 16 * (CB * c.wave + j) + (lane >> 2);
     const int grow = min(n0 + row, N - 1);
-    const int ck = (lane & 3) ^ (row & 3);  // logical chunk stored at physical chunk lane & 3
+    const int ck = (lane & 3) ^ wt_swizzle(row);  // logical chunk stored at physical chunk lane & 3
     c.wsrc[j] = w + size_t(grow) * K + ck * 16;
   }
-  int colsum = 0;
-  v16i acc[4][2];
+  int colsum[CB];
+  v16i acc[4][CB];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int cb = 0; cb < CB; ++cb) {
+    colsum[cb] = 0;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16i{0};
+    for (int rb = 0; rb < 4; ++rb) acc[rb][cb] = v16i{0};
+  }
 
   // split-K: workgroup z takes K steps [z k_split, (z+1) k_split); with more
   // than one split the partial products are added into y (zeroed first) by
   // 64-bit atomics, exact mod 2^64 in any order
   const int k_begin = split_z * k_split;
   const int steps = min(k_split, K - k_begin) / kBK;
-  dma_issue(c, k_begin, raw0, wt0);
-  for (int s = 0; s < steps; s += 2) {
-    dma_step(c, s + 1 < steps, k_begin + (s + 1) * kBK, raw0, wt0, raw1, wt1, a_lds, colsum, acc);
-    if (s + 1 < steps)
-      dma_step(c, s + 2 < steps, k_begin + (s + 2) * kBK, raw1, wt1, raw0, wt0, a_lds, colsum, acc);
+  if constexpr (CB == 3) {
+    auto raw_of = [&](int q) { return q == 0 ? raw0 : (q == 1 ? raw1 : raw2); };
+    auto wt_of = [&](int q) { return q == 0 ? wt0 : (q == 1 ? wt1 : wt2); };
+    // steps 0..2 in flight (past the last step: the last step's tile again)
+    dma_issue<CB>(c, k_begin, raw0, wt0);
+    dma_issue<CB>(c, k_begin + min(1, steps - 1) * kBK, raw1, wt1);
+    dma_issue<CB>(c, k_begin + min(2, steps - 1) * kBK, raw2, wt2);
+    asm volatile("s_waitcnt vmcnt(14)\n\ts_barrier" ::: "memory");
+    HalfOps<CB> h0, h1;
+    read_half<CB>(c, 0, raw0, wt0, h0);
+    int q = 0;  // stage of step s
+    for (int s = 0; s < steps; ++s) {
+      const int qn = q == 2 ? 0 : q + 1;
+      piped_step<CB>(c, s, steps, k_begin, raw_of(q), wt_of(q), raw_of(qn), wt_of(qn), h0, h1, colsum, acc);
+      q = qn;
+    }
+    // the refills past the last step land before the workgroup ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+  dma_issue<CB>(c, k_begin, raw0, wt0);
+  if (steps > 1) dma_issue<CB>(c, k_begin + kBK, raw1, wt1);
+  for (int s = 0; s < steps; s += 3) {
+    const int kn = k_begin + (s + 2) * kBK;
+    dma_step<CB>(c, s + 1 < steps, s + 2 < steps, kn, raw0, wt0, raw2, wt2, colsum, acc);
+    if (s + 1 < steps) dma_step<CB>(c, s + 2 < steps, s + 3 < steps, kn + kBK, raw1, wt1, raw0, wt0, colsum, acc);
+    if (s + 2 < steps) dma_step<CB>(c, s + 3 < steps, s + 4 < steps, kn + 2 * kBK, raw2, wt2, raw1, wt1, colsum, acc);
+  }
   }
   const bool split = gridDim.z > 1;
 
   // ---- epilogue: column sums, digit recombination, shift, mask
-  csum[t] = colsum;
-  __syncthreads();
   const int i = c.i, khalf = c.khalf, wm = c.wm, wn = c.wn;
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int c2 = wn * 64 + cb * 32 + i;
+  for (int cb = 0; cb < CB; ++cb) {
+    const int c2 = wn * 32 * CB + cb * 32 + i;
     const int col = n0 + c2;
-    if (col >= N) continue;
-    const int64_t s_n = int64_t(csum[2 * c2]) + int64_t(csum[2 * c2 + 1]);
+    if (col >= N) continue;  // the same for lanes l and l ^ 32
+    const int64_t s_n = int64_t(colsum[cb]) + __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, colsum[cb]);
     const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
     const int sh = 8 * plane + (shifts ? int(shifts[col]) : 0);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
+      // register group g: share row g of the block, digits 4 khalf .. 4 khalf + 3
+      uint64_t part[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        // sum_ii acc_ii 256^ii fits 56 signed bits: three 32x32+64 MADs
+        const int64_t v = int64_t(acc[rb][cb][4 * g]) + int64_t(acc[rb][cb][4 * g + 1]) * 256 +
+                          int64_t(acc[rb][cb][4 * g + 2]) * 65536 + int64_t(acc[rb][cb][4 * g + 3]) * 16777216;
+        part[g] = uint64_t(v) << (32 * khalf);
+      }
+      // this half writes rows 2 khalf, 2 khalf + 1 and sends the other two
+      const uint64_t own0 = khalf ? part[2] : part[0], own1 = khalf ? part[3] : part[1];
+      const uint64_t give0 = khalf ? part[0] : part[2], give1 = khalf ? part[1] : part[3];
+      const uint64_t sum0 = own0 + swap_halves(give0, lane), sum1 = own1 + swap_halves(give1, lane);
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int row = m0 + wm * 16 + rb * 4 + 2 * khalf + a;
         if (row >= M) continue;
-        uint64_t v = corr;
-#pragma unroll
-        for (int dg = 0; dg < 8; ++dg) v += uint64_t(int64_t(acc[rb][cb][8 * a + dg])) << (8 * dg);
+        uint64_t v = corr + (a ? sum1 : sum0);
         v = sh < 64 ? (v << sh) : 0;
         if (split)
           atomicAdd(reinterpret_cast<unsigned long long*>(y + size_t(row) * N + col), (unsigned long long)v);
@@ -562,15 +749,22 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
   if (w_bits == 8 || w_bits == 24) {
     const int planes = w_bits == 8 ? 1 : 3;
     if (K % kBK == 0 && w_vec && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-      // Split K while the tiles fill fewer than 256 workgroups (one per CU;
-      // N = 1024 at M = 512 gives 128 tiles) and each split keeps >= 8 steps:
-      // measured 37 -> 26 us at 512x2048x1024 and 54 -> 33 us at 512x3072x1024,
-      // while going on to two workgroups per CU was slower.
-      const int tiles = int(grid.x * grid.y), ksteps = K / kBK;
-      int splits = 1;
-      while (splits < 4 && tiles * splits < 256 && ksteps / (splits * 2) >= 8) splits *= 2;
-      const int k_split = (ksteps + splits - 1) / splits * kBK;
-      splits = (K + k_split - 1) / k_split;
+      // 128-column tiles (CB = 2, up to two workgroups per CU), K split while
+      // the tiles fill fewer than 256 workgroups and each split keeps >= 8
+      // steps.  192-column tiles (CB = 3, one workgroup per CU) only where
+      // they fill the 256 CUs in one round while the 128-column grid would
+      // leave the CUs unevenly loaded (between one and two workgroups each):
+      // 512 x 1024 x 3072 int8 runs 21.4 us against 22.8 us; every other
+      // Qwen3 shape and the f12 planes run faster with CB = 2 (measured).
+      const int ksteps = K / kBK;
+      const long tiles2 = long((N + 127) / 128) * long((M + kBM - 1) / kBM);
+      const long tiles3 = long((N + 191) / 192) * long((M + kBM - 1) / kBM);
+      int best_splits = 1;
+      while (best_splits < 4 && tiles2 * best_splits < 256 && ksteps / (best_splits * 2) >= 8) best_splits *= 2;
+      const long wg2 = tiles2 * best_splits * planes;
+      const int best_cb = (best_splits == 1 && planes == 1 && wg2 > 256 && wg2 < 512 && tiles3 <= 256) ? 3 : 2;
+      const int k_split = (ksteps + best_splits - 1) / best_splits * kBK;
+      const int splits = (K + k_split - 1) / k_split;
       const size_t words = size_t(M) * N;
       const unsigned fgrid = unsigned(std::min<size_t>((words + 255) / 256, 4096));
       // several planes or K splits add their partial products into y
@@ -580,8 +774,13 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
       }
-      hipLaunchKernelGGL(share_gemm_dma_kernel, dim3(grid.x, grid.y, unsigned(splits * planes)), block, 0, s, x,
-                         static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split, splits);
+      const unsigned gy = unsigned((M + kBM - 1) / kBM), gz = unsigned(splits * planes);
+      if (best_cb == 2)
+        hipLaunchKernelGGL(share_gemm_dma_kernel<2>, dim3(unsigned((N + 127) / 128), gy, gz), block, 0, s, x,
+                           static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split, splits);
+      else
+        hipLaunchKernelGGL(share_gemm_dma_kernel<3>, dim3(unsigned((N + 191) / 192), gy, gz), block, 0, s, x,
+                           static_cast<const int8_t*>(w), shifts, y, M, K, N, mask, k_split, splits);
       hipError_t e = hipGetLastError();
       if (e == hipSuccess && atomic && mask != ~0ull) {
         hipLaunchKernelGGL(gemm_clear_kernel, dim3(fgrid), dim3(256), 0, s, y, words, mask);

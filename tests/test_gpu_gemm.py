@@ -92,6 +92,19 @@ def test_gemm_split_k_shapes(gpu, m, k, n):
         np.testing.assert_array_equal(_run(x, w, shifts, mask), oracle.share_gemm(x, w, shifts, mask))
 
 
+@pytest.mark.parametrize("m,k,n", [(512, 1024, 3072), (500, 1024, 3000), (481, 640, 2900)])
+def test_gemm_wide_tiles(gpu, m, k, n):
+    """Shapes whose 128-column grid would load the CUs unevenly run 192-column
+    tiles with one workgroup per CU (the pipelined kernel): ragged rows and
+    columns, shifts and the 59-bit ring included."""
+    print(f"[gemm] wide tiles m={m} k={k} n={n}", flush=True)
+    x = oracle.fill_u64(m * k, 9000 + n).reshape(m, k)
+    w = oracle.fill_i8(n * k, 9100 + n).reshape(n, k)
+    sh = oracle.fill_shift(n, 9200 + n)
+    for shifts, mask in ((None, 64), (sh, 59)):
+        np.testing.assert_array_equal(_run(x, w, shifts, mask), oracle.share_gemm(x, w, shifts, mask))
+
+
 def test_gemm_c4_f12_presplit(gpu, tmp_path):
     """C4's shape with the reference's weight domain (int32 f12, |w| <= 2^20,
     quantize_weights.py:91,102) pre-split into three signed-byte planes: once
