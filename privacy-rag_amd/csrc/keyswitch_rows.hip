@@ -65,6 +65,20 @@ __device__ __forceinline__ uint64_t gather(const uint64_t* __restrict__ limb, un
   return ((i >> kLog) && v) ? q - v : v;
 }
 
+// Column c (coefficients c + 1024 k, k < 16) of a limb after the Galois
+// gather; a plain strided read when the element is the identity (ginv is a
+// launch argument, so the branch is uniform).
+__device__ __forceinline__ void gather_column(uint64_t (&y)[kE], const uint64_t* __restrict__ limb, unsigned c,
+                                              uint32_t ginv, uint64_t q) {
+  if (ginv == 1) {
+#pragma unroll
+    for (int k = 0; k < kE; ++k) y[k] = limb[c + (unsigned(k) << kRowLog)];
+  } else {
+#pragma unroll
+    for (int k = 0; k < kE; ++k) y[k] = gather(limb, c + (unsigned(k) << kRowLog), ginv, q);
+  }
+}
+
 // Stored form of a policy value: doubles by their bits, integers as they are.
 template <class A>
 __device__ __forceinline__ uint64_t store_form(typename A::T x) {
@@ -97,20 +111,25 @@ __device__ __forceinline__ const typename A::TW* inv_table(const KsRows& f, int 
 }
 
 // ------------------------------------------------------------------ phase A
-// Waves per SIMD the column kernels are compiled for: the float path fits
-// three, the integer path's 64-bit products need the registers of two.
-template <class A>
-constexpr int kColWaves() {
-  return std::is_same<typename A::T, double>::value ? 3 : 2;
+// Waves per SIMD the forward column kernels are compiled for (the twiddles
+// live in scalar registers): one-prime digits need only the 16 values, four
+// fit; the base conversion of two- and three-prime digits needs the registers
+// of two.
+template <int D>
+constexpr int kColFwdWaves() {
+  return D == 1 ? 4 : 2;
 }
 
 // Twiddles of forward stages 0-3 in the order fwd_pass consumes them: one
 // group per stage (stage s uses fwd[2^s + k], k < 2^s), i.e. fwd[1..15].
-template <class A>
+// kScalar: the twiddles are moved to scalar registers (the table index is
+// wave-uniform), which frees their VGPRs where the SGPRs are not needed for
+// more than one target's values.
+template <class A, bool kScalar>
 __device__ __forceinline__ void top_fwd(typename A::T (&v)[kE], const typename A::TW* __restrict__ tab, const A& ar) {
   typename A::TW w[pass_twiddles<kLogE>()];
 #pragma unroll
-  for (int n = 0; n < pass_twiddles<kLogE>(); ++n) w[n] = tab[1 + n];
+  for (int n = 0; n < pass_twiddles<kLogE>(); ++n) w[n] = kScalar ? to_sgpr(tab[1 + n]) : tab[1 + n];
   fwd_pass<kLog, kLog - kLogE, kLogE>(v, w, ar, [] {});
 }
 
@@ -205,7 +224,12 @@ __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, un
   const unsigned groups = (t_n + G - 1) / G;
   const unsigned gid = blk * blockDim.x + threadIdx.x;
   if (gid >= f.cts * dnum * groups * kCols) return;
-  const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;  // w is uniform per wave
+  // kCols is a multiple of the wave size, so w is the same for every lane of
+  // a wave; on the integer path readfirstlane lets the targets' twiddle pairs
+  // live in scalar registers (the float path keeps its six targets' in VGPRs)
+  unsigned w = gid >> kRowLog;
+  if constexpr (!std::is_same<typename A::T, double>::value) w = __builtin_amdgcn_readfirstlane(w);
+  const unsigned c = gid & (kCols - 1);
   const unsigned g = w % groups, j = (w / groups) % dnum, bl = w / (groups * dnum), b = f.b0 + bl;
   const int lo = kc.dig_lo[j];
   const uint64_t* c1 = f.in + ((size_t(b) * 2 + 1) * L << kLog);
@@ -214,8 +238,7 @@ __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, un
   if constexpr (D == 1) {
     // one prime per digit: (Q_j / q_i) = 1, so the digit expands to its own
     // canonical residues, reduced mod each target below
-#pragma unroll
-    for (int k = 0; k < kE; ++k) y[0][k] = gather(c1 + (size_t(lo) << kLog), c + (unsigned(k) << kRowLog), f.ginv, kc.q[lo]);
+    gather_column(y[0], c1 + (size_t(lo) << kLog), c, f.ginv, kc.q[lo]);
   } else if (G > 1) {
     digit_factors<D, A>(y, f, kc, c1, lo, c);
   }
@@ -242,7 +265,7 @@ __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, un
       else
         cols_target_u64<D>(v, y, kc, lo, int(t));
     }
-    top_fwd<A>(v, fwd_table<A>(f, int(t)), ar);
+    top_fwd<A, D == 1>(v, fwd_table<A>(f, int(__builtin_amdgcn_readfirstlane(t))), ar);  // t is wave-uniform
     uint64_t* et = f.e + ((size_t(bl) * dnum + j) * K + t) * kN + c;
 #pragma unroll
     for (int k = 0; k < kE; ++k) et[unsigned(k) << kRowLog] = store_form<A>(v[k]);
@@ -251,7 +274,7 @@ __device__ __forceinline__ void cols_fwd_body(const KsRows& f, unsigned t_lo, un
 
 // One policy per launch (every prime on the integer path).
 template <int D, class A, unsigned G>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColFwdWaves<D>())))
     ks_cols_fwd_kernel(KsRows f, unsigned t_lo, unsigned t_n) {
   cols_fwd_body<D, A, G>(f, t_lo, t_n, blockIdx.x);
 }
@@ -261,7 +284,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWa
 // float-path data primes, so the special prime's 64-bit work overlaps the
 // float targets instead of running after them.
 template <int D>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1 ? 3 : 2)))
     ks_cols_fwd_both(KsRows f, unsigned t_u64, unsigned n_u64, unsigned nu) {
   if (blockIdx.x < nu) cols_fwd_body<D, ArU64, 1>(f, t_u64, n_u64, blockIdx.x);
   else cols_fwd_body<D, ArF64Lean, kColTargets<ArF64Lean>()>(f, 0u, t_u64, blockIdx.x - nu);
@@ -497,7 +520,7 @@ __device__ __forceinline__ void top_inv(typename A::T (&v)[kE], const typename A
     const int l = kLog - kLogE + i;
 #pragma unroll
     for (int k = 0; k < (1 << (kLogE - 1 - i)); ++k) {
-      if (l != kLog - 1) w[n] = tab[kN - (kN >> l) + 1 + k];
+      if (l != kLog - 1) w[n] = to_sgpr(tab[kN - (kN >> l) + 1 + k]);
       ++n;
     }
   }
@@ -520,12 +543,12 @@ __device__ __forceinline__ void column_residues(uint64_t (&x)[kE], const uint64_
 // Special-prime limbs first: one thread per (ciphertext, component,
 // column) finishes the inverse transform and leaves [P_p + floor(p/2)]_p in
 // place of the limb, the rounding term every data prime's ModDown reads.
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) ks_cols_special_kernel(KsRows f) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) ks_cols_special_kernel(KsRows f) {
   const KsConst& kc = *f.kc;
   const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
   const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= f.cts * 2 * kCols) return;
-  const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;
+  const unsigned c = gid & (kCols - 1), w = __builtin_amdgcn_readfirstlane(gid >> kRowLog);
   const unsigned comp = w & 1u, b = f.b0 + (w >> 1);
   uint64_t* pl = f.prod + ((size_t(b) * 2 + comp) * K + L) * kN + c;
   const uint64_t p = kc.q[L], half = p >> 1;
@@ -541,13 +564,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
 // Then one thread per (ciphertext, component, data prime, column) finishes
 // that prime's inverse transform (policy A) and applies ModDown (+ c0).
 template <class A>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWaves<A>())))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(std::is_same<typename A::T, double>::value ? 3 : 4)))
     ks_cols_inv_kernel(KsRows f) {
   const KsConst& kc = *f.kc;
   const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
   const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= f.cts * 2 * L * kCols) return;
-  const unsigned c = gid & (kCols - 1), w = gid >> kRowLog;
+  const unsigned c = gid & (kCols - 1), w = __builtin_amdgcn_readfirstlane(gid >> kRowLog);
   const unsigned i = w % L, comp = (w / L) & 1u, b = f.b0 + w / (2 * L);
   const uint64_t* pc = f.prod + ((size_t(b) * 2 + comp) * K << kLog) + c;
   const uint64_t qi = kc.q[i];
@@ -568,8 +591,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWa
       for (int k = 0; k < kE; ++k) v[k] = double_of(pc[(size_t(i) << kLog) + (unsigned(k) << kRowLog)]);
 #pragma unroll
       for (int k = 0; k < kE; ++k) lastv[k] = pc[(size_t(L) << kLog) + (unsigned(k) << kRowLog)];
+      if (comp == 0) {
+        gather_column(c0v, c0, c, f.ginv, qi);
+      } else {
 #pragma unroll
-      for (int k = 0; k < kE; ++k) c0v[k] = comp == 0 ? gather(c0, c + (unsigned(k) << kRowLog), f.ginv, qi) : 0;
+        for (int k = 0; k < kE; ++k) c0v[k] = 0;
+      }
       top_inv<ArF64>(v, f.tw_inv_f + (size_t(i) << kLog), ar, pi);
       const double c32 = 4294967296.0, c32q = c32 * pi.qinv;
       const double ip = double(kc.invp[i].w), ipq = ip * pi.qinv, half = double(kc.half_mod[i]);
@@ -585,15 +612,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColWa
       return;
     }
   }
-  uint64_t x[kE];
+  uint64_t x[kE], c0v[kE];
   column_residues<A>(x, pc + (size_t(i) << kLog), inv_table<A>(f, int(i)), f.primes[i]);
+  if (comp == 0) gather_column(c0v, c0, c, f.ginv, qi);
 #pragma unroll
   for (int k = 0; k < kE; ++k) {
     const uint64_t last = pc[(size_t(L) << kLog) + (unsigned(k) << kRowLog)];
     const uint64_t reduced = reduce_to(last, kc, int(i), f.narrow);  // last mod q_i
     const uint64_t corr = sub_mod(reduced, kc.half_mod[i], qi);
     uint64_t val = mul_shoup(sub_mod(x[k], corr, qi), kc.invp[i].w, kc.invp[i].wq, qi);
-    if (comp == 0) val = add_mod(val, gather(c0, c + (unsigned(k) << kRowLog), f.ginv, qi), qi);
+    if (comp == 0) val = add_mod(val, c0v[k], qi);
     o[unsigned(k) << kRowLog] = val;
   }
 }

@@ -43,6 +43,37 @@ struct NttPrime {
 
 __host__ __device__ __forceinline__ unsigned lds_pos(unsigned x) { return x + (x >> 4); }
 
+// Load of a twiddle (or other table word) that no kernel writes while it runs,
+// through the constant address space: when the address is the same for every
+// lane of the wave the compiler issues it as a scalar load into SGPRs, whatever
+// stores the kernel makes elsewhere.
+template <class T>
+__device__ __forceinline__ T load_invariant(const T* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return *(const __attribute__((address_space(4))) T*)p;
+#else
+  return *p;  // host pass: never executed
+#endif
+}
+
+// A value that is the same in every lane (a twiddle loaded from a wave-uniform
+// address), moved into scalar registers so it takes no VGPRs.
+__device__ __forceinline__ uint64_t sgpr_u64(uint64_t x) {
+  // readfirstlane returns int: zero-extend each half
+  const unsigned hi = unsigned(__builtin_amdgcn_readfirstlane(unsigned(x >> 32)));
+  const unsigned lo = unsigned(__builtin_amdgcn_readfirstlane(unsigned(x)));
+  return (uint64_t(hi) << 32) | lo;
+}
+__device__ __forceinline__ double to_sgpr(double x) {
+  return __longlong_as_double((long long)sgpr_u64((uint64_t)__double_as_longlong(x)));
+}
+__device__ __forceinline__ ulonglong2 to_sgpr(ulonglong2 x) {
+  ulonglong2 r;
+  r.x = sgpr_u64(x.x);
+  r.y = sgpr_u64(x.y);
+  return r;
+}
+
 constexpr int kLogE = 4;  // 16 coefficients per thread
 constexpr int kE = 1 << kLogE;
 
@@ -241,17 +272,18 @@ __device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<Passes<
     // twiddle loads go through the scalar unit into SGPRs.
     const unsigned hi_lane = M::elem(t, b << R) >> (LO + R);
     const unsigned hi = M::uniform_groups() ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
+    const auto ld = [&](unsigned x) { return M::uniform_groups() ? load_invariant(tab + x) : tab[x]; };
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       if (!INV) {
         const int s = LOGN - LO - R + i;
 #pragma unroll
-        for (int k = 0; k < (1 << i); ++k) w[n++] = tab[(1u << s) + (hi << i) + k];
+        for (int k = 0; k < (1 << i); ++k) w[n++] = ld((1u << s) + (hi << i) + k);
       } else {
         const int l = LO + i;
 #pragma unroll
         for (int k = 0; k < (1 << (R - 1 - i)); ++k) {
-          if (l != LOGN - 1) w[n] = tab[N - (N >> l) + 1 + (hi << (R - 1 - i)) + k];
+          if (l != LOGN - 1) w[n] = ld(N - (N >> l) + 1 + (hi << (R - 1 - i)) + k);
           ++n;
         }
       }
