@@ -648,6 +648,20 @@ int build_ks_const(const uint64_t* q, size_t L, size_t dnum, unsigned log_n, KsC
     kc.invp[i] = Shoup{ip, shoup_q(ip, q[i])};
     kc.half_mod[i] = (p >> 1) % q[i];
   }
+  kc.lazy = 1;
+  const uint64_t n = 1ull << log_n;
+  std::vector<uint64_t> fwd(2 * n), inv(2 * n), invn(2);
+  for (size_t t = 0; t < K; ++t) {
+    kc.lazy &= q[t] < (1ull << 60) ? 1 : 0;
+    uint64_t y = 1;  // q^-1 mod 2^64 by Newton's iteration (each step doubles the correct low bits)
+    for (int it = 0; it < 6; ++it) y *= 2 - q[t] * y;
+    kc.neg_qinv[t] = 0 - y;
+    if (!make_tables(q[t], log_n, fwd.data(), inv.data(), invn.data(), nullptr)) return PRAGHIP_E_CONTEXT;
+    const uint64_t r = uint64_t(((u128)1 << 64) % q[t]);  // 2^64 mod q_t
+    const uint64_t nr = mulmod(invn[0], r, q[t]), lr = mulmod(inv[2 * (n - 1)], nr, q[t]);
+    kc.ninv_r[t] = Shoup{nr, shoup_q(nr, q[t])};
+    kc.last_r[t] = Shoup{lr, shoup_q(lr, q[t])};
+  }
   return PRAGHIP_OK;
 }
 }  // namespace praghip::host

@@ -43,6 +43,12 @@ struct KsConst {
   Shoup invp[kMaxKeyPrimes];             // p^-1 mod q_i
   uint64_t half_mod[kMaxKeyPrimes];      // floor(p/2) mod q_i
   uint64_t one_q[kMaxKeyPrimes];         // floor(2^64 / q_t): Shoup constant of 1, every key prime
+  // lazy integer path (every key prime below 2^60): Montgomery key products,
+  // whose factor 2^-64 the last inverse stage removes
+  int lazy;
+  uint64_t neg_qinv[kMaxKeyPrimes];      // -q_t^-1 mod 2^64
+  Shoup ninv_r[kMaxKeyPrimes];           // N^-1 2^64 mod q_t
+  Shoup last_r[kMaxKeyPrimes];           // w_last N^-1 2^64 mod q_t (w_last = inv[N-1])
 };
 
 struct KsArgs {

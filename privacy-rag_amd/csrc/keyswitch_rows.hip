@@ -280,13 +280,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColFw
 }
 
 // Both policies in one launch when both are present: the first nu blocks
-// take the integer-path primes t_u64 .. t_u64 + n_u64 - 1, the rest the
-// float-path data primes, so the special prime's 64-bit work overlaps the
-// float targets instead of running after them.
-template <int D>
+// take the integer-path primes t_u64 .. t_u64 + n_u64 - 1 (policy AU: ArU64L
+// when every key prime is below 2^60, else ArU64), the rest the float-path
+// data primes, so the special prime's 64-bit work overlaps the float targets
+// instead of running after them.
+template <int D, class AU>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1 ? 3 : 2)))
     ks_cols_fwd_both(KsRows f, unsigned t_u64, unsigned n_u64, unsigned nu) {
-  if (blockIdx.x < nu) cols_fwd_body<D, ArU64, 1>(f, t_u64, n_u64, blockIdx.x);
+  if (blockIdx.x < nu) cols_fwd_body<D, AU, 1>(f, t_u64, n_u64, blockIdx.x);
   else cols_fwd_body<D, ArF64Lean, kColTargets<ArF64Lean>()>(f, 0u, t_u64, blockIdx.x - nu);
 }
 
@@ -389,6 +390,35 @@ __device__ __forceinline__ void row_mac_u64(uint64_t (&v)[kE], uint64_t (&a0)[kE
   }
 }
 
+// Key products of the lazy integer path (ArU64L, every key prime below 2^60):
+// Montgomery products x k 2^-64 of the transformed digit word (x < 12q after
+// stage 13) and the canonical key words (x k < 12 q^2 < q 2^64, so each
+// product is below 2q), added without reduction; the sums start at zero and
+// are reduced by 8q after every fourth digit, so they stay below 16q.  The
+// last inverse stage multiplies the factor 2^64 back in (mont_prime).
+__device__ __forceinline__ void row_mac_mont(const uint64_t (&v)[kE], uint64_t (&a0)[kE], uint64_t (&a1)[kE],
+                                             const uint64_t* __restrict__ k0, const uint64_t* __restrict__ k1,
+                                             unsigned lane, unsigned row, uint64_t q, uint64_t nq) {
+#pragma unroll
+  for (int r = 0; r < kE; r += 2) {
+    const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog>(lane, r);
+    const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+    const ulonglong2 kb = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = r + h;
+      a0[rr] += mul_mont(v[rr], h ? ka.y : ka.x, q, nq);
+      a1[rr] += mul_mont(v[rr], h ? kb.y : kb.x, q, nq);
+    }
+    if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__device__ __forceinline__ void reduce_by(uint64_t (&a)[kE], uint64_t m) {
+#pragma unroll
+  for (int k = 0; k < kE; ++k) a[k] = a[k] >= m ? a[k] - m : a[k];
+}
+
 template <class A>
 __device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t, unsigned row,
                                          unsigned lane, typename A::T* lds) {
@@ -400,7 +430,12 @@ __device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, uns
   const typename A::TW* tf = fwd_table<A>(f, int(t));
   const typename A::TW* ti = inv_table<A>(f, int(t));
   const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
+  constexpr bool kMont = std::is_same<A, ArU64L>::value;
   T a0[kE], a1[kE];
+  if constexpr (kMont) {
+#pragma unroll
+    for (int k = 0; k < kE; ++k) a0[k] = a1[k] = 0;
+  }
   for (unsigned j = 0; j < dnum; ++j) {
     const uint64_t* src = f.e + ((size_t(bl) * dnum + j) * K + t) * kN + (row << kRowLog);
     T v[kE];
@@ -409,9 +444,23 @@ __device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, uns
     row_transform<false>(v, lds, lane, row, tf, ar, pr);
     const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << kLog);
     const uint64_t* k1 = k0 + (size_t(K) << kLog);
-    row_mac_u64(v, a0, a1, k0, k1, lane, row, j == 0, ar, kc.bar[t]);
+    if constexpr (kMont) {
+      row_mac_mont(v, a0, a1, k0, k1, lane, row, ar.q, kc.neg_qinv[t]);
+      if ((j & 3) == 3) {
+        reduce_by(a0, ar.q8);
+        reduce_by(a1, ar.q8);
+      }
+    } else {
+      row_mac_u64(v, a0, a1, k0, k1, lane, row, j == 0, ar, kc.bar[t]);
+    }
     // the next digit's first exchange writes the LDS this digit's last one read
     __builtin_amdgcn_wave_barrier();
+  }
+  if constexpr (kMont) {  // below 16q -> below 4q, the lazy inverse's input bound
+    reduce_by(a0, ar.q8);
+    reduce_by(a0, ar.q4);
+    reduce_by(a1, ar.q8);
+    reduce_by(a1, ar.q4);
   }
   uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
   row_transform<true>(a0, lds, lane, row, ti, ar, pr);
@@ -485,6 +534,7 @@ constexpr unsigned kRowWaves = 4;  // waves (items) per workgroup
 // integer-path primes t_u64 .. K - 1 (the special prime, or every prime when
 // a data prime has 50 bits or more) and go first, being the longest; the rest
 // are the float-path data primes 0 .. t_u64 - 1.
+template <class AU>
 __global__ void __launch_bounds__(64 * kRowWaves) __attribute__((amdgpu_waves_per_eu(2)))
     ks_rows_kernel(KsRows f, unsigned t_u64) {
   __shared__ __attribute__((aligned(16))) uint64_t lds_all[kRowWaves * kRowLds];
@@ -499,7 +549,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) __attribute__((amdgpu_waves_pe
   uint64_t* lds = lds_all + wave * kRowLds;
   if (item < u64_items) {
     const unsigned row = item % rows, t = t_u64 + (item / rows) % n_u64, bl = item / (rows * n_u64);
-    row_item<ArU64>(f, kc, bl, t, row, lane, lds);
+    row_item<AU>(f, kc, bl, t, row, lane, lds);
   } else {
     const unsigned x = item - u64_items;
     const unsigned row = x % rows, t = (x / rows) % t_u64, bl = x / (rows * t_u64);
@@ -527,6 +577,21 @@ __device__ __forceinline__ void top_inv(typename A::T (&v)[kE], const typename A
   inv_pass<kLog, kLog - kLogE, kLogE>(v, w, ar, pr, [] {});
 }
 
+// Constants of key prime t for the last inverse stage of a product formed
+// by Montgomery key products (the lazy integer path): N^-1 and w_last N^-1
+// carry the factor 2^64 that the products lack.
+template <class A>
+__device__ __forceinline__ NttPrime product_prime(const KsRows& f, const KsConst& kc, int t) {
+  NttPrime r = f.primes[t];
+  if constexpr (std::is_same<A, ArU64L>::value) {
+    r.ninv = kc.ninv_r[t].w;
+    r.ninv_q = kc.ninv_r[t].wq;
+    r.last = kc.last_r[t].w;
+    r.last_q = kc.last_r[t].wq;
+  }
+  return r;
+}
+
 // Canonical coefficient-form residues of one product limb at column c.
 template <class A>
 __device__ __forceinline__ void column_residues(uint64_t (&x)[kE], const uint64_t* __restrict__ src,
@@ -543,6 +608,7 @@ __device__ __forceinline__ void column_residues(uint64_t (&x)[kE], const uint64_
 // Special-prime limbs first: one thread per (ciphertext, component,
 // column) finishes the inverse transform and leaves [P_p + floor(p/2)]_p in
 // place of the limb, the rounding term every data prime's ModDown reads.
+template <class AU>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) ks_cols_special_kernel(KsRows f) {
   const KsConst& kc = *f.kc;
   const unsigned K = unsigned(kc.K), L = unsigned(kc.L);
@@ -553,7 +619,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) k
   uint64_t* pl = f.prod + ((size_t(b) * 2 + comp) * K + L) * kN + c;
   const uint64_t p = kc.q[L], half = p >> 1;
   uint64_t last[kE];
-  column_residues<ArU64>(last, pl, f.tw_inv_u + (size_t(L) << kLog), f.primes[L]);
+  column_residues<AU>(last, pl, f.tw_inv_u + (size_t(L) << kLog), product_prime<AU>(f, kc, int(L)));
 #pragma unroll
   for (int k = 0; k < kE; ++k) {
     const uint64_t x = last[k] + half;
@@ -613,7 +679,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(std::i
     }
   }
   uint64_t x[kE], c0v[kE];
-  column_residues<A>(x, pc + (size_t(i) << kLog), inv_table<A>(f, int(i)), f.primes[i]);
+  column_residues<A>(x, pc + (size_t(i) << kLog), inv_table<A>(f, int(i)), product_prime<A>(f, kc, int(i)));
   if (comp == 0) gather_column(c0v, c0, c, f.ginv, qi);
 #pragma unroll
   for (int k = 0; k < kE; ++k) {
@@ -636,16 +702,41 @@ static int uniform_digit(const KsConst& kc) {
   return d;
 }
 
-template <int D>
+template <int D, class AU>
 static void launch_cols_fwd(const KsRows& f, unsigned dnum, unsigned t_u64, unsigned K, hipStream_t s) {
   const auto grid = [&](unsigned t_n, unsigned g) { return dim3((f.cts * dnum * ((t_n + g - 1) / g) * kCols + 255) / 256); };
   constexpr unsigned GU = kColTargets<ArU64>(), GF = kColTargets<ArF64Lean>();
   if (!t_u64) {  // every prime on the integer path
-    hipLaunchKernelGGL((ks_cols_fwd_kernel<D, ArU64, GU>), grid(K, GU), dim3(256), 0, s, f, 0u, K);
+    hipLaunchKernelGGL((ks_cols_fwd_kernel<D, AU, GU>), grid(K, GU), dim3(256), 0, s, f, 0u, K);
     return;
   }
   const unsigned nu = grid(K - t_u64, GU).x, nf = grid(t_u64, GF).x;
-  hipLaunchKernelGGL((ks_cols_fwd_both<D>), dim3(nu + nf), dim3(256), 0, s, f, t_u64, K - t_u64, nu);
+  hipLaunchKernelGGL((ks_cols_fwd_both<D, AU>), dim3(nu + nf), dim3(256), 0, s, f, t_u64, K - t_u64, nu);
+}
+
+// One chunk of ciphertexts through the four launches, the integer-path
+// primes on policy AU.
+template <class AU>
+static void launch_chunk(const KsRows& f, const KsConst& kc, int dig, hipStream_t s) {
+  const unsigned K = unsigned(kc.K), L = unsigned(kc.L), dnum = unsigned(kc.dnum), rows = kN >> kRowLog;
+  // the integer-path primes t_u64 .. K - 1 (the special prime, or every
+  // prime when a data prime has 50 bits or more), the float-path data
+  // primes below t_u64
+  const unsigned t_u64 = f.data_f64 ? L : 0;
+  switch (dig) {
+    case 1: launch_cols_fwd<1, AU>(f, dnum, t_u64, K, s); break;
+    case 2: launch_cols_fwd<2, AU>(f, dnum, t_u64, K, s); break;
+    default: launch_cols_fwd<3, AU>(f, dnum, t_u64, K, s); break;
+  }
+  const unsigned items = f.cts * K * rows;
+  hipLaunchKernelGGL(ks_rows_kernel<AU>, dim3((items + kRowWaves - 1) / kRowWaves), dim3(64 * kRowWaves), 0, s, f,
+                     t_u64);
+  hipLaunchKernelGGL(ks_cols_special_kernel<AU>, dim3((f.cts * 2 * kCols + 255) / 256), dim3(256), 0, s, f);
+  const dim3 c_grid((f.cts * 2 * L * kCols + 255) / 256);
+  if (f.data_f64)
+    hipLaunchKernelGGL(ks_cols_inv_kernel<ArF64>, c_grid, dim3(256), 0, s, f);
+  else
+    hipLaunchKernelGGL(ks_cols_inv_kernel<AU>, c_grid, dim3(256), 0, s, f);
 }
 
 bool keyswitch_rows_supported(const KsConst& kc) {
@@ -684,28 +775,15 @@ hipError_t launch_keyswitch_rows(const KsArgs& a, const KsConst* kc_dev, const K
     q_min = std::min(q_min, kc.q[t]);
   }
   f.narrow = q_max / 2 < q_min ? 1 : 0;  // q_max < 2 q_min
-  const unsigned K = unsigned(kc.K), L = unsigned(kc.L), dnum = unsigned(kc.dnum), rows = kN >> kRowLog;
   for (size_t b0 = 0; b0 < a.batch; b0 += a.inter_cts) {
     f.b0 = unsigned(b0);
     f.cts = unsigned(std::min<size_t>(a.inter_cts, a.batch - b0));
-    // the integer-path primes t_u64 .. K - 1 (the special prime, or every
-    // prime when a data prime has 50 bits or more), the float-path data
-    // primes below t_u64
-    const unsigned t_u64 = f.data_f64 ? L : 0;
-    switch (dig) {
-      case 1: launch_cols_fwd<1>(f, dnum, t_u64, K, s); break;
-      case 2: launch_cols_fwd<2>(f, dnum, t_u64, K, s); break;
-      default: launch_cols_fwd<3>(f, dnum, t_u64, K, s); break;
-    }
-    const unsigned items = f.cts * K * rows;
-    hipLaunchKernelGGL(ks_rows_kernel, dim3((items + kRowWaves - 1) / kRowWaves), dim3(64 * kRowWaves), 0, s, f,
-                       t_u64);
-    hipLaunchKernelGGL(ks_cols_special_kernel, dim3((f.cts * 2 * kCols + 255) / 256), dim3(256), 0, s, f);
-    const dim3 c_grid((f.cts * 2 * L * kCols + 255) / 256);
-    if (f.data_f64)
-      hipLaunchKernelGGL(ks_cols_inv_kernel<ArF64>, c_grid, dim3(256), 0, s, f);
+    // every key prime below 2^60: the lazy integer path with Montgomery key
+    // products (KsConst::lazy); else Harvey's bounds and Shoup key products
+    if (kc.lazy)
+      launch_chunk<ArU64L>(f, kc, dig, s);
     else
-      hipLaunchKernelGGL(ks_cols_inv_kernel<ArU64>, c_grid, dim3(256), 0, s, f);
+      launch_chunk<ArU64>(f, kc, dig, s);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

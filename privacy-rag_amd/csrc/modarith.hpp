@@ -73,6 +73,16 @@ PH_HD uint64_t mul_barrett(uint64_t a, uint64_t b, const Barrett m) {
   return r >= m.q ? r - m.q : r;
 }
 
+// Montgomery product with R = 2^64: x k 2^-64 mod q, in [0, 2q) whenever
+// x k < q 2^64 (nq = -q^-1 mod 2^64).  m = (x k mod 2^64) nq makes x k + m q
+// a multiple of 2^64; its low word cancels the low word of x k with a carry
+// exactly when that low word is non-zero, and (x k + m q) / 2^64 < 2q.
+PH_HD uint64_t mul_mont(uint64_t x, uint64_t k, uint64_t q, uint64_t nq) {
+  const uint64_t lo = x * k, hi = mulhi64(x, k);
+  const uint64_t m = lo * nq;
+  return hi + mulhi64(m, q) + uint64_t(lo != 0);
+}
+
 // floor(w 2^64 / q) for w < q, from the Barrett ratio R = floor((2^128-1)/q):
 // t = w r1 + floor(w r0 / 2^64) = floor(w R / 2^64) fits 64 bits (w r1 < 2^64)
 // and is the quotient or one less, since R > 2^128/q - 1 and w < 2^64; the

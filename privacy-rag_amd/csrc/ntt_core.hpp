@@ -96,6 +96,7 @@ struct ArU64 {
     x = a + t;
     y = a - t + q2;
   }
+  __device__ __forceinline__ void fwd_at(int, T& x, T& y, TW w) const { fwd(x, y, w); }
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {  // GS, values in [0,2q)
     T s = x + y;
     s = s >= q2 ? s - q2 : s;
@@ -112,6 +113,46 @@ struct ArU64 {
   // Harvey's bounds hold without re-centring
   static constexpr bool settle_fwd(int) { return false; }
   static constexpr bool settle_inv(int) { return false; }
+};
+
+// The integer path for q < 2^60, where 16q < 2^64 leaves room for lazier
+// bounds than Harvey's:
+//   forward - a butterfly's X input is reduced by 8q (when at or above 8q)
+//             only at stages s = 4, 8, 12, ...; every other stage adds at most
+//             2q to the bound (X + T and X - T + 2q, Shoup product T < 2q).
+//             From inputs below 8q the values after stage s are below
+//             8q + 2q (1 + s mod 4) <= 16q (10q, 12q, 14q, 16q, 10q, ...);
+//   inverse - values below 4q: the sum reduced by 4q, the difference offset
+//             by 4q before its Shoup product; the last stage's products are
+//             below 2q.
+struct ArU64L : ArU64 {
+  uint64_t q4, q8;
+  __device__ explicit ArU64L(const NttPrime& p) : ArU64(p), q4(4 * p.q), q8(8 * p.q) {}
+  __device__ __forceinline__ uint64_t to_u64_fwd(T x) const {  // [0,16q) -> [0,q)
+    x = x >= q8 ? x - q8 : x;
+    x = x >= q4 ? x - q4 : x;
+    x = x >= q2 ? x - q2 : x;
+    return x >= q ? x - q : x;
+  }
+  __device__ __forceinline__ void fwd_at(int s, T& x, T& y, TW w) const {
+    T a = x;
+    if (s > 0 && s % 4 == 0) a = a >= q8 ? a - q8 : a;
+    const T t = mul_shoup_lazy(y, w.x, w.y, q);
+    x = a + t;
+    y = a - t + q2;
+  }
+  __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
+    T s = x + y;
+    s = s >= q4 ? s - q4 : s;
+    const T d = x - y + q4;
+    x = s;
+    y = mul_shoup_lazy(d, w.x, w.y, q);
+  }
+  __device__ __forceinline__ void inv_last(T& x, T& y, const NttPrime& p) const {
+    const T s = x + y, d = x - y + q4;
+    x = mul_shoup_lazy(s, p.ninv, p.ninv_q, q);
+    y = mul_shoup_lazy(d, p.last, p.last_q, q);
+  }
 };
 
 // Float path bounds (q < 2^50, |x| <= M q, mul_f64 gives |t| <= (1/2 + 3A/8) q
@@ -149,6 +190,7 @@ struct ArF64 {
     x = a + t;
     y = a - t;
   }
+  __device__ __forceinline__ void fwd_at(int, T& x, T& y, TW w) const { fwd(x, y, w); }
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
     const T s = x + y, d = x - y;
     x = s;
@@ -316,7 +358,7 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename 
 #pragma unroll
         for (int m = 0; m < (1 << g); ++m) {
           const int j0 = (b << R) | (k << (g + 1)) | m, j1 = j0 | (1 << g);
-          ar.fwd(v[j0], v[j1], w[n]);
+          ar.fwd_at(s, v[j0], v[j1], w[n]);
         }
       }
       if (A::settle_fwd(s) && s != LOGN - 1) {  // the final stage is reduced on output
