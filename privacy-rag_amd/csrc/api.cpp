@@ -250,6 +250,7 @@ hipError_t upload_ntt(const NttHost& h, unsigned log_n, Buffers& buf, NttDevice&
       d.host_sel_f64[d.n_f64++] = int(p);
     else
       d.host_sel_u64[d.n_u64++] = int(p);
+    if (!h.primes[p].use_f64 && h.primes[p].q >= (1ull << 60)) d.lazy_u64 = 0;
   }
   if ((e = buf.alloc((void**)&d.sel_f64, 64 * sizeof(int), false)) != hipSuccess) return e;
   if ((e = buf.alloc((void**)&d.sel_u64, 64 * sizeof(int), false)) != hipSuccess) return e;

@@ -23,6 +23,7 @@ struct NttDevice {
   int* sel_u64 = nullptr;            // device [n_u64]
   int n_f64 = 0, n_u64 = 0;
   int host_sel_f64[64] = {}, host_sel_u64[64] = {};
+  int lazy_u64 = 1;  // every integer-path prime below 2^60: the lazy integer transforms (ArU64L)
 };
 
 hipError_t launch_ntt(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d, hipStream_t s);

@@ -122,19 +122,26 @@ static hipError_t launch_subset(uint64_t* data, size_t limbs, const NttDevice& d
   return hipGetLastError();
 }
 
+template <class A>
+struct TypeTag {
+  using type = A;
+};
+
 template <int LOGN>
 static hipError_t launch_ntt_n(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d,
                                hipStream_t s) {
+  // integer-path primes all below 2^60: the lazy transforms (ArU64L)
+  const auto u64 = [&](auto tag, bool inv) {
+    using A = typename decltype(tag)::type;
+    return inv ? launch_subset<LOGN, true, A>(data, limbs, d, d.tw_inv_u, d.sel_u64, d.host_sel_u64, d.n_u64, s)
+               : launch_subset<LOGN, false, A>(data, limbs, d, d.tw_fwd_u, d.sel_u64, d.host_sel_u64, d.n_u64, s);
+  };
   hipError_t e;
-  if (inverse) {
+  if (inverse)
     e = launch_subset<LOGN, true, ArF64>(data, limbs, d, d.tw_inv_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
-    if (e == hipSuccess)
-      e = launch_subset<LOGN, true, ArU64>(data, limbs, d, d.tw_inv_u, d.sel_u64, d.host_sel_u64, d.n_u64, s);
-  } else {
+  else
     e = launch_subset<LOGN, false, ArF64>(data, limbs, d, d.tw_fwd_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
-    if (e == hipSuccess)
-      e = launch_subset<LOGN, false, ArU64>(data, limbs, d, d.tw_fwd_u, d.sel_u64, d.host_sel_u64, d.n_u64, s);
-  }
+  if (e == hipSuccess && d.n_u64) e = d.lazy_u64 ? u64(TypeTag<ArU64L>{}, inverse) : u64(TypeTag<ArU64>{}, inverse);
   return e;
 }
 
