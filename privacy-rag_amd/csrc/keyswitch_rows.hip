@@ -7,7 +7,7 @@
 //               0-3 (gaps 8192..1024): thread c holds coefficients
 //               c + 1024 k, k = 0..15, and every twiddle is the same for all
 //               threads.  Out: E[b][j][t][N] (lazy, per-policy form).
-//   B  rows     one wave per (ciphertext, prime t, row r): forward stages
+//   B  rows     two waves per (ciphertext, prime t, row r): forward stages
 //               4-13 of each digit's row, the key product summed over the
 //               digits in registers, inverse stages 0-9 of both sums.
 //               Out: the products' rows, [b][2][K][N] (lazy).
@@ -292,17 +292,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1
 }
 
 // ------------------------------------------------------------------ phase B
-// Twiddles of row pass P (a 1024-coefficient transform's pass map, with the
-// row's bits above it): global group index = (row << 10 | local) >> (LO + R).
-template <bool INV, int P, class TW>
-__device__ __forceinline__ void row_twiddles(TW (&w)[pass_twiddles<Passes<kRowLog>::r(INV, P)>()], unsigned lane,
-                                             unsigned row, const TW* __restrict__ tab) {
-  using M = PassMap<kRowLog, INV, P>;
-  constexpr int LO = M::LO, R = M::R, SUB = kE >> R;
+// One item = (ciphertext, key prime t, row of 1024 coefficients) on the two
+// waves of a workgroup, 8 coefficients per lane (radix-8 register passes, one
+// exchange crossing the two waves, the others within a wave): forward stages
+// 4-13 of each digit's row, the key products summed over the digits in
+// registers, inverse stages 0-9 of both sums.  Eight coefficients per lane
+// keep a wave within 168 VGPRs, so a SIMD holds three waves.
+constexpr int kRowLE = 3;                           // 8 coefficients per lane
+constexpr unsigned kRow2Threads = 1u << (kRowLog - kRowLE);  // 128: the item's two waves
+
+// Twiddles of row pass P (a 1024-coefficient transform's pass map with 2^LE
+// coefficients per thread, the row's bits above it): global group index =
+// (row << 10 | local) >> (LO + R); t is the thread of the item.
+template <bool INV, int P, int LE, class TW>
+__device__ __forceinline__ void row_twiddles_e(TW (&w)[(pass_tw_count<kRowLog, INV, P, LE>())], unsigned t,
+                                               unsigned row, const TW* __restrict__ tab) {
+  using M = PassMap<kRowLog, INV, P, LE>;
+  constexpr int LO = M::LO, R = M::R, SUB = (1 << LE) >> R;
   int n = 0;
 #pragma unroll
   for (int b = 0; b < SUB; ++b) {
-    const unsigned hi_lane = ((row << kRowLog) | M::elem(lane, b << R)) >> (LO + R);
+    const unsigned hi_lane = ((row << kRowLog) | M::elem(t, b << R)) >> (LO + R);
     const unsigned hi = M::uniform_groups() ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -319,110 +329,46 @@ __device__ __forceinline__ void row_twiddles(TW (&w)[pass_twiddles<Passes<kRowLo
   }
 }
 
-template <bool INV, int P, class A>
-__device__ __forceinline__ void row_pass(typename A::T (&v)[kE], unsigned lane, unsigned row,
-                                         const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr) {
-  using S = Passes<kRowLog>;
+// Passes P .. NP - 1 of a row on 2^LE coefficients per thread, each pass's
+// twiddles loaded when it starts; stage numbers are the N = 16384
+// transform's.
+template <bool INV, int P, class A, int E>
+__device__ __forceinline__ void row_passes_e(typename A::T (&v)[E], typename A::T* lds, unsigned t, unsigned row,
+                                             const typename A::TW* __restrict__ tab, const A& ar, const NttPrime& pr) {
+  constexpr int LE = ilog2(E);
+  using S = Passes<kRowLog, LE>;
   constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
-  typename A::TW w[pass_twiddles<R>()];
-  row_twiddles<INV, P>(w, lane, row, tab);
-  // stage numbers are the N = 16384 transform's: no row stage is the last
-  // inverse stage, and the re-centring points are the whole transform's
+  typename A::TW w[pass_tw_count<kRowLog, INV, P, LE>()];
+  row_twiddles_e<INV, P, LE>(w, t, row, tab);
   if constexpr (INV)
     inv_pass<kLog, LO, R>(v, w, ar, pr, [] {});
   else
     fwd_pass<kLog, LO, R>(v, w, ar, [] {});
-}
-
-template <bool INV, class A>
-__device__ __forceinline__ void row_transform(typename A::T (&v)[kE], typename A::T* lds, unsigned lane, unsigned row,
-                                              const typename A::TW* __restrict__ tab, const A& ar,
-                                              const NttPrime& pr) {
-  if constexpr (A::kAhead) {
-    // each pass's twiddles are loaded halfway through the pass before
-    using S = Passes<kRowLog>;
-    using TW = typename A::TW;
-    TW w0[pass_twiddles<S::r(INV, 0)>()], w1[pass_twiddles<S::r(INV, 1)>()], w2[pass_twiddles<S::r(INV, 2)>()];
-    row_twiddles<INV, 0>(w0, lane, row, tab);
-    const auto pass = [&](auto p, auto& w, auto&& mid) {
-      constexpr int P = decltype(p)::value, LO = S::lo(INV, P), R = S::r(INV, P);
-      if constexpr (INV)
-        inv_pass<kLog, LO, R>(v, w, ar, pr, mid);
-      else
-        fwd_pass<kLog, LO, R>(v, w, ar, mid);
-    };
-    pass(std::integral_constant<int, 0>{}, w0, [&] { row_twiddles<INV, 1>(w1, lane, row, tab); });
-    exchange<kRowLog, INV, 0>(v, lds, lane);
-    pass(std::integral_constant<int, 1>{}, w1, [&] { row_twiddles<INV, 2>(w2, lane, row, tab); });
-    exchange<kRowLog, INV, 1>(v, lds, lane);
-    pass(std::integral_constant<int, 2>{}, w2, [] {});
-  } else {
-    row_pass<INV, 0>(v, lane, row, tab, ar, pr);
-    exchange<kRowLog, INV, 0>(v, lds, lane);
-    row_pass<INV, 1>(v, lane, row, tab, ar, pr);
-    exchange<kRowLog, INV, 1>(v, lds, lane);
-    row_pass<INV, 2>(v, lane, row, tab, ar, pr);
+  if constexpr (P + 1 < S::NP) {
+    exchange<kRowLog, INV, P>(v, lds, t);
+    row_passes_e<INV, P + 1>(v, lds, t, row, tab, ar, pr);
   }
 }
 
-__device__ __forceinline__ void row_mac_u64(uint64_t (&v)[kE], uint64_t (&a0)[kE], uint64_t (&a1)[kE],
-                                            const uint64_t* __restrict__ k0, const uint64_t* __restrict__ k1,
-                                            unsigned lane, unsigned row, bool first, const ArU64& ar,
-                                            const Barrett& bar) {
-#pragma unroll
-  for (int r = 0; r < kE; r += 2) {
-    const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog>(lane, r);
-    const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
-    const ulonglong2 kb = *reinterpret_cast<const ulonglong2*>(k1 + pos);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int rr = r + h;
-      // the transformed digit word meets two key words: one Shoup quotient,
-      // two Shoup products
-      const uint64_t x = ar.to_u64_fwd(v[rr]);
-      const uint64_t xq = shoup_quotient(x, bar);
-      const uint64_t p0 = mul_shoup(h ? ka.y : ka.x, x, xq, ar.q);
-      const uint64_t p1 = mul_shoup(h ? kb.y : kb.x, x, xq, ar.q);
-      a0[rr] = first ? p0 : add_mod(a0[rr], p0, ar.q);
-      a1[rr] = first ? p1 : add_mod(a1[rr], p1, ar.q);
-    }
-    if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// Key products of the lazy integer path (ArU64L, every key prime below 2^60):
-// Montgomery products x k 2^-64 of the transformed digit word (x < 12q after
-// stage 13) and the canonical key words (x k < 12 q^2 < q 2^64, so each
-// product is below 2q), added without reduction; the sums start at zero and
-// are reduced by 8q after every fourth digit, so they stay below 16q.  The
-// last inverse stage multiplies the factor 2^64 back in (mont_prime).
-__device__ __forceinline__ void row_mac_mont(const uint64_t (&v)[kE], uint64_t (&a0)[kE], uint64_t (&a1)[kE],
-                                             const uint64_t* __restrict__ k0, const uint64_t* __restrict__ k1,
-                                             unsigned lane, unsigned row, uint64_t q, uint64_t nq) {
-#pragma unroll
-  for (int r = 0; r < kE; r += 2) {
-    const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog>(lane, r);
-    const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
-    const ulonglong2 kb = *reinterpret_cast<const ulonglong2*>(k1 + pos);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int rr = r + h;
-      a0[rr] += mul_mont(v[rr], h ? ka.y : ka.x, q, nq);
-      a1[rr] += mul_mont(v[rr], h ? kb.y : kb.x, q, nq);
-    }
-    if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-__device__ __forceinline__ void reduce_by(uint64_t (&a)[kE], uint64_t m) {
-#pragma unroll
-  for (int k = 0; k < kE; ++k) a[k] = a[k] >= m ? a[k] - m : a[k];
-}
-
+// Item (ciphertext bl, prime t, row) on the two waves of the workgroup
+// (thread t2 < 128).  Policy A:
+//   ArU64L    - every key prime below 2^60: Montgomery key products x k 2^-64
+//               of the transformed digit word (x < 12q after stage 13) and
+//               the canonical key words (x k < 12 q^2 < q 2^64, each product
+//               below 2q), added without reduction from zero and reduced by 8q
+//               after every fourth digit, so the sums stay below 16q; the last
+//               inverse stage multiplies the factor 2^64 back in
+//               (product_prime);
+//   ArU64     - Harvey bounds: the transformed digit word meets two key words,
+//               so it gets one Shoup quotient and two Shoup products;
+//   ArF64Lean - the float data primes (q < 2^50), exact FP64 products.
 template <class A>
-__device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t, unsigned row,
-                                         unsigned lane, typename A::T* lds) {
+__device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t,
+                                          unsigned row, unsigned t2, typename A::T* lds) {
   using T = typename A::T;
+  constexpr int E = 1 << kRowLE;
+  constexpr bool kF64 = std::is_same<T, double>::value;
+  constexpr bool kMont = std::is_same<A, ArU64L>::value;
   const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K);
   const unsigned b = f.b0 + bl;
   const NttPrime pr = f.primes[t];
@@ -430,130 +376,101 @@ __device__ __forceinline__ void row_item(const KsRows& f, const KsConst& kc, uns
   const typename A::TW* tf = fwd_table<A>(f, int(t));
   const typename A::TW* ti = inv_table<A>(f, int(t));
   const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
-  constexpr bool kMont = std::is_same<A, ArU64L>::value;
-  T a0[kE], a1[kE];
+  T a0[E], a1[E];
   if constexpr (kMont) {
 #pragma unroll
-    for (int k = 0; k < kE; ++k) a0[k] = a1[k] = 0;
+    for (int k = 0; k < E; ++k) a0[k] = a1[k] = 0;
   }
   for (unsigned j = 0; j < dnum; ++j) {
     const uint64_t* src = f.e + ((size_t(bl) * dnum + j) * K + t) * kN + (row << kRowLog);
-    T v[kE];
+    T v[E];
 #pragma unroll
-    for (int k = 0; k < kE; ++k) v[k] = load_form<A>(src[fwd_in_index<kRowLog>(lane, k)]);
-    row_transform<false>(v, lds, lane, row, tf, ar, pr);
-    const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << kLog);
-    const uint64_t* k1 = k0 + (size_t(K) << kLog);
-    if constexpr (kMont) {
-      row_mac_mont(v, a0, a1, k0, k1, lane, row, ar.q, kc.neg_qinv[t]);
-      if ((j & 3) == 3) {
-        reduce_by(a0, ar.q8);
-        reduce_by(a1, ar.q8);
-      }
-    } else {
-      row_mac_u64(v, a0, a1, k0, k1, lane, row, j == 0, ar, kc.bar[t]);
-    }
-    // the next digit's first exchange writes the LDS this digit's last one read
-    __builtin_amdgcn_wave_barrier();
-  }
-  if constexpr (kMont) {  // below 16q -> below 4q, the lazy inverse's input bound
-    reduce_by(a0, ar.q8);
-    reduce_by(a0, ar.q4);
-    reduce_by(a1, ar.q8);
-    reduce_by(a1, ar.q4);
-  }
-  uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
-  row_transform<true>(a0, lds, lane, row, ti, ar, pr);
-#pragma unroll
-  for (int k = 0; k < kE; ++k) pb[inv_out_index<kRowLog>(lane, k)] = store_form<A>(a0[k]);
-  __builtin_amdgcn_wave_barrier();
-  row_transform<true>(a1, lds, lane, row, ti, ar, pr);
-  uint64_t* pc = pb + (size_t(K) << kLog);
-#pragma unroll
-  for (int k = 0; k < kE; ++k) pc[inv_out_index<kRowLog>(lane, k)] = store_form<A>(a1[k]);
-}
-
-// The float-path row item (each pass's twiddles loaded halfway through the
-// pass before).  (Loading a digit's key words before its forward
-// transform, or the next digit's row before the key product, does not pay:
-// vector loads complete in order, so each pass's twiddle wait also waits for
-// the early loads, and the extra registers spill.)
-__device__ __forceinline__ void row_item_f64(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t, unsigned row,
-                                             unsigned lane, double* lds) {
-  using A = ArF64;
-  const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K);
-  const unsigned b = f.b0 + bl;
-  const NttPrime pr = f.primes[t];
-  const A ar(pr);
-  const double* tf = f.tw_fwd_f + (size_t(t) << kLog);
-  const double* ti = f.tw_inv_f + (size_t(t) << kLog);
-  const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
-  const uint64_t* e0 = f.e + (size_t(bl) * dnum * K + t) * kN + (row << kRowLog);
-  const size_t e_digit = size_t(K) * kN;
-  double a0[kE], a1[kE];
-  for (unsigned j = 0; j < dnum; ++j) {
-    double v[kE];
-#pragma unroll
-    for (int k = 0; k < kE; ++k) v[k] = double_of(e0[j * e_digit + fwd_in_index<kRowLog>(lane, k)]);
-    row_transform<false>(v, lds, lane, row, tf, ar, pr);
+    for (int k = 0; k < E; ++k) v[k] = load_form<A>(src[fwd_in_index<kRowLog, kRowLE>(t2, k)]);
+    row_passes_e<false, 0>(v, lds, t2, row, tf, ar, pr);
     const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << kLog);
     const uint64_t* k1 = k0 + (size_t(K) << kLog);
 #pragma unroll
-    for (int r = 0; r < kE; r += 2) {
+    for (int r = 0; r < E; r += 2) {
       // registers r, r + 1 hold adjacent coefficients after the last forward
       // pass: one 16-byte load per key limb
-      const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog>(lane, r);
-      const ulonglong2 x = *reinterpret_cast<const ulonglong2*>(k0 + pos);
-      const ulonglong2 y = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+      const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog, kRowLE>(t2, r);
+      const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+      const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(k1 + pos);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        // |v| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
-        const double p0 = ar.mul(v[r + h], ArF64::from_u64(h ? x.y : x.x));
-        const double p1 = ar.mul(v[r + h], ArF64::from_u64(h ? y.y : y.x));
-        a0[r + h] = reduce_f64(j ? a0[r + h] + p0 : p0, ar.q, ar.qinv);
-        a1[r + h] = reduce_f64(j ? a1[r + h] + p1 : p1, ar.q, ar.qinv);
+        const int rr = r + h;
+        const uint64_t w0 = h ? ka.y : ka.x, w1 = h ? kk.y : kk.x;
+        if constexpr (kF64) {
+          // |v| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
+          const double p0 = ar.mul(v[rr], ArF64::from_u64(w0));
+          const double p1 = ar.mul(v[rr], ArF64::from_u64(w1));
+          a0[rr] = reduce_f64(j ? a0[rr] + p0 : p0, ar.q, ar.qinv);
+          a1[rr] = reduce_f64(j ? a1[rr] + p1 : p1, ar.q, ar.qinv);
+        } else if constexpr (kMont) {
+          // x < 12q after stage 13, canonical key words: each product < 2q
+          a0[rr] += mul_mont(v[rr], w0, ar.q, kc.neg_qinv[t]);
+          a1[rr] += mul_mont(v[rr], w1, ar.q, kc.neg_qinv[t]);
+        } else {
+          const uint64_t x = ar.to_u64_fwd(v[rr]);
+          const uint64_t xq = shoup_quotient(x, kc.bar[t]);
+          const uint64_t p0 = mul_shoup(w0, x, xq, ar.q), p1 = mul_shoup(w1, x, xq, ar.q);
+          a0[rr] = j ? add_mod(a0[rr], p0, ar.q) : p0;
+          a1[rr] = j ? add_mod(a1[rr], p1, ar.q) : p1;
+        }
       }
     }
-    // the next digit's first exchange writes the LDS this digit's last one read
-    __builtin_amdgcn_wave_barrier();
+    if constexpr (kMont) {
+      if ((j & 3) == 3) {  // sums below 16q: reduced by 8q every fourth digit
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+          a0[k] = a0[k] >= ar.q8 ? a0[k] - ar.q8 : a0[k];
+          a1[k] = a1[k] >= ar.q8 ? a1[k] - ar.q8 : a1[k];
+        }
+      }
+    }
+    // the next digit's first exchange writes the LDS this digit's last one
+    // read, and crosses the waves: it starts with a workgroup barrier
+  }
+  if constexpr (kMont) {  // below 16q -> below 4q, the lazy inverse's input bound
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      a0[k] = a0[k] >= ar.q8 ? a0[k] - ar.q8 : a0[k];
+      a0[k] = a0[k] >= ar.q4 ? a0[k] - ar.q4 : a0[k];
+      a1[k] = a1[k] >= ar.q8 ? a1[k] - ar.q8 : a1[k];
+      a1[k] = a1[k] >= ar.q4 ? a1[k] - ar.q4 : a1[k];
+    }
   }
   uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
-  row_transform<true>(a0, lds, lane, row, ti, ar, pr);
+  row_passes_e<true, 0>(a0, lds, t2, row, ti, ar, pr);
 #pragma unroll
-  for (int k = 0; k < kE; ++k) pb[inv_out_index<kRowLog>(lane, k)] = bits_of(a0[k]);
-  __builtin_amdgcn_wave_barrier();
-  row_transform<true>(a1, lds, lane, row, ti, ar, pr);
+  for (int k = 0; k < E; ++k) pb[inv_out_index<kRowLog, kRowLE>(t2, k)] = store_form<A>(a0[k]);
+  __syncthreads();  // the second transform's first exchange reuses the LDS
+  row_passes_e<true, 0>(a1, lds, t2, row, ti, ar, pr);
   uint64_t* pc = pb + (size_t(K) << kLog);
 #pragma unroll
-  for (int k = 0; k < kE; ++k) pc[inv_out_index<kRowLog>(lane, k)] = bits_of(a1[k]);
+  for (int k = 0; k < E; ++k) pc[inv_out_index<kRowLog, kRowLE>(t2, k)] = store_form<A>(a1[k]);
 }
 
-constexpr unsigned kRowWaves = 4;  // waves (items) per workgroup
-
-// One wave per (ciphertext, prime t, row).  Items [0, u64_items) are the
-// integer-path primes t_u64 .. K - 1 (the special prime, or every prime when
-// a data prime has 50 bits or more) and go first, being the longest; the rest
-// are the float-path data primes 0 .. t_u64 - 1.
+// One workgroup (two waves) per item; items [0, u64_items) are the
+// integer-path primes t_u64 .. K - 1 (policy AU), the rest the float-path data
+// primes 0 .. t_u64 - 1.
 template <class AU>
-__global__ void __launch_bounds__(64 * kRowWaves) __attribute__((amdgpu_waves_per_eu(2)))
-    ks_rows_kernel(KsRows f, unsigned t_u64) {
-  __shared__ __attribute__((aligned(16))) uint64_t lds_all[kRowWaves * kRowLds];
+__global__ void __launch_bounds__(kRow2Threads) __attribute__((amdgpu_waves_per_eu(3)))
+    ks_rows2_kernel(KsRows f, unsigned t_u64) {
+  __shared__ __attribute__((aligned(16))) uint64_t lds[kRowLds];
   const KsConst& kc = *f.kc;
   const unsigned K = unsigned(kc.K);
-  const unsigned lane = threadIdx.x & 63u;
-  const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const unsigned item = blockIdx.x * kRowWaves + wave;
+  const unsigned item = blockIdx.x, t2 = threadIdx.x;
   constexpr unsigned rows = kN >> kRowLog;
   const unsigned n_u64 = K - t_u64, u64_items = f.cts * n_u64 * rows;
   if (item >= f.cts * K * rows) return;
-  uint64_t* lds = lds_all + wave * kRowLds;
   if (item < u64_items) {
     const unsigned row = item % rows, t = t_u64 + (item / rows) % n_u64, bl = item / (rows * n_u64);
-    row_item<AU>(f, kc, bl, t, row, lane, lds);
+    row_item2<AU>(f, kc, bl, t, row, t2, lds);
   } else {
     const unsigned x = item - u64_items;
     const unsigned row = x % rows, t = (x / rows) % t_u64, bl = x / (rows * t_u64);
-    row_item_f64(f, kc, bl, t, row, lane, reinterpret_cast<double*>(lds));
+    row_item2<ArF64Lean>(f, kc, bl, t, row, t2, reinterpret_cast<double*>(lds));
   }
 }
 
@@ -729,8 +646,7 @@ static void launch_chunk(const KsRows& f, const KsConst& kc, int dig, hipStream_
     default: launch_cols_fwd<3, AU>(f, dnum, t_u64, K, s); break;
   }
   const unsigned items = f.cts * K * rows;
-  hipLaunchKernelGGL(ks_rows_kernel<AU>, dim3((items + kRowWaves - 1) / kRowWaves), dim3(64 * kRowWaves), 0, s, f,
-                     t_u64);
+  hipLaunchKernelGGL(ks_rows2_kernel<AU>, dim3(items), dim3(kRow2Threads), 0, s, f, t_u64);
   hipLaunchKernelGGL(ks_cols_special_kernel<AU>, dim3((f.cts * 2 * kCols + 255) / 256), dim3(256), 0, s, f);
   const dim3 c_grid((f.cts * 2 * L * kCols + 255) / 256);
   if (f.data_f64)

@@ -213,27 +213,28 @@ struct ArF64Lean : ArF64 {
   __device__ explicit ArF64Lean(const NttPrime& p) : ArF64(p) {}
 };
 
-// Pass geometry.  Forward passes take 4 gap bits from the top down, the last
-// one the remainder [0, RSHORT); inverse passes start with the remainder
-// [0, RSHORT) and continue upwards 4 bits at a time.
-template <int LOGN>
+// Pass geometry, for 2^LE coefficients per thread (LE = 4 unless a caller
+// asks for fewer).  Forward passes take LE gap bits from the top down, the
+// last one the remainder [0, RSHORT); inverse passes start with the remainder
+// [0, RSHORT) and continue upwards LE bits at a time.
+template <int LOGN, int LE = kLogE>
 struct Passes {
-  static constexpr int NP = (LOGN + kLogE - 1) / kLogE;
-  static constexpr int RSHORT = LOGN - kLogE * (NP - 1);
-  static constexpr int fwd_lo(int p) { return p < NP - 1 ? LOGN - kLogE * (p + 1) : 0; }
-  static constexpr int fwd_r(int p) { return p < NP - 1 ? kLogE : RSHORT; }
-  static constexpr int inv_lo(int p) { return p == 0 ? 0 : RSHORT + kLogE * (p - 1); }
-  static constexpr int inv_r(int p) { return p == 0 ? RSHORT : kLogE; }
+  static constexpr int NP = (LOGN + LE - 1) / LE;
+  static constexpr int RSHORT = LOGN - LE * (NP - 1);
+  static constexpr int fwd_lo(int p) { return p < NP - 1 ? LOGN - LE * (p + 1) : 0; }
+  static constexpr int fwd_r(int p) { return p < NP - 1 ? LE : RSHORT; }
+  static constexpr int inv_lo(int p) { return p == 0 ? 0 : RSHORT + LE * (p - 1); }
+  static constexpr int inv_r(int p) { return p == 0 ? RSHORT : LE; }
   static constexpr int lo(bool inv, int p) { return inv ? inv_lo(p) : fwd_lo(p); }
   static constexpr int r(bool inv, int p) { return inv ? inv_r(p) : fwd_r(p); }
-  static constexpr int LANE_BITS = LOGN - kLogE < 6 ? LOGN - kLogE : 6;  // thread bits inside a wave
-  static constexpr int WAVE_BITS = LOGN - kLogE - LANE_BITS;             // thread bits naming the wave
+  static constexpr int LANE_BITS = LOGN - LE < 6 ? LOGN - LE : 6;  // thread bits inside a wave
+  static constexpr int WAVE_BITS = LOGN - LE - LANE_BITS;          // thread bits naming the wave
 };
 
-// Placement of a thread's 16 registers in a pass.  The coefficient index is
+// Placement of a thread's 2^LE registers in a pass.  The coefficient index is
 // assembled from three fields:
-//   register bits - the pass's gap bits [LO, LO+R), and when R < 4 (LO = 0
-//                   then) 4 - R bits just below the wave bits for the
+//   register bits - the pass's gap bits [LO, LO+R), and when R < LE (LO = 0
+//                   then) LE - R bits just below the wave bits for the
 //                   independent blocks;
 //   wave bits     - the top WAVE_BITS bits, except in the pass whose gap bits
 //                   are the top bits, where they sit just below them;
@@ -246,15 +247,15 @@ struct Passes {
 // coefficients (coalesced global access); the last forward and first inverse
 // pass give each lane runs of 2^R consecutive coefficients, consecutive lanes
 // on consecutive runs.
-template <int LOGN, bool INV, int P>
+template <int LOGN, bool INV, int P, int LE = kLogE>
 struct PassMap {
-  using S = Passes<LOGN>;
+  using S = Passes<LOGN, LE>;
   static constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
   static constexpr int WAVE_LO = (LO + R == LOGN) ? LO - S::WAVE_BITS : LOGN - S::WAVE_BITS;
-  // block bits (R < 4, LO = 0): just below the wave bits
-  static constexpr int BLOCK_LO = WAVE_LO - (kLogE - R);
+  // block bits (R < LE, LO = 0): just below the wave bits
+  static constexpr int BLOCK_LO = WAVE_LO - (LE - R);
   static constexpr int reg_bit(int q) { return q < R ? LO + q : BLOCK_LO + (q - R); }
-  static constexpr bool is_reg(int e) { return (e >= LO && e < LO + R) || (e >= BLOCK_LO && e < WAVE_LO && R < kLogE); }
+  static constexpr bool is_reg(int e) { return (e >= LO && e < LO + R) || (e >= BLOCK_LO && e < WAVE_LO && R < LE); }
   static constexpr bool is_wave(int e) { return e >= WAVE_LO && e < WAVE_LO + S::WAVE_BITS; }
   static constexpr int lane_bit(int q) {
     int c = 0;
@@ -274,7 +275,7 @@ struct PassMap {
   }
   __host__ __device__ static constexpr unsigned reg_field(int j) {
     unsigned x = 0;
-    for (int q = 0; q < kLogE; ++q) x |= unsigned((j >> q) & 1) << reg_bit(q);
+    for (int q = 0; q < LE; ++q) x |= unsigned((j >> q) & 1) << reg_bit(q);
     return x;
   }
   __host__ __device__ static unsigned thread_field(unsigned t) {
@@ -297,14 +298,23 @@ struct PassMap {
 // ------------------------------------------------------------------ passes
 // Twiddles of one pass: SUB blocks x (2^R - 1) entries, in the order the pass
 // consumes them (block, stage, group).
-template <int R>
-constexpr int pass_twiddles() { return (kE >> R) * ((1 << R) - 1); }
+template <int R, int LE = kLogE>
+constexpr int pass_twiddles() { return ((1 << LE) >> R) * ((1 << R) - 1); }
 
-template <int LOGN, bool INV, int P, class TW>
-__device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<Passes<LOGN>::r(INV, P)>()], unsigned t,
-                                                   const TW* __restrict__ tab) {
-  using M = PassMap<LOGN, INV, P>;
-  constexpr int LO = M::LO, R = M::R, SUB = kE >> R;
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
+
+// Twiddles of pass P of a 2^LOGN transform with 2^LE coefficients per thread.
+template <int LOGN, bool INV, int P, int LE>
+constexpr int pass_tw_count() {
+  constexpr int R = Passes<LOGN, LE>::r(INV, P);
+  return pass_twiddles<R, LE>();
+}
+
+template <int LOGN, bool INV, int P, int LE, class TW>
+__device__ __forceinline__ void load_pass_twiddles_e(TW (&w)[(pass_tw_count<LOGN, INV, P, LE>())], unsigned t,
+                                                     const TW* __restrict__ tab) {
+  using M = PassMap<LOGN, INV, P, LE>;
+  constexpr int LO = M::LO, R = M::R, SUB = (1 << LE) >> R;
   constexpr unsigned N = 1u << LOGN;
   int n = 0;
 #pragma unroll
@@ -332,21 +342,26 @@ __device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<Passes<
     }
   }
 }
+template <int LOGN, bool INV, int P, class TW>
+__device__ __forceinline__ void load_pass_twiddles(TW (&w)[pass_twiddles<Passes<LOGN>::r(INV, P)>()], unsigned t,
+                                                   const TW* __restrict__ tab) {
+  load_pass_twiddles_e<LOGN, INV, P, kLogE>(w, t, tab);
+}
 
 // Forward radix-2^R pass over gap bits [LO, LO+R): global stages
 // s = LOGN-LO-R .. LOGN-LO-1.
 // A pass calls `mid` once, halfway through its butterflies (after stage R/2-1
 // of a single block, or after block SUB/2-1): the twiddles of the early stages
 // are dead by then, which is where the next pass's twiddle loads go.
-template <int R>
+template <int R, int LE = kLogE>
 __device__ __forceinline__ constexpr bool is_mid(int b, int i) {
-  return (kE >> R) == 1 ? (i == R / 2 - 1) : (b == (kE >> R) / 2 - 1 && i == R - 1);
+  return ((1 << LE) >> R) == 1 ? (i == R / 2 - 1) : (b == ((1 << LE) >> R) / 2 - 1 && i == R - 1);
 }
 
-template <int LOGN, int LO, int R, class A, class F>
-__device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename A::TW (&w)[pass_twiddles<R>()],
+template <int LOGN, int LO, int R, class A, class F, int E>
+__device__ __forceinline__ void fwd_pass(typename A::T (&v)[E], const typename A::TW (&w)[pass_twiddles<R, ilog2(E)>()],
                                          const A& ar, F&& mid) {
-  constexpr int SUB = kE >> R;
+  constexpr int LE = ilog2(E), SUB = E >> R;
   int n = 0;
 #pragma unroll
   for (int b = 0; b < SUB; ++b) {
@@ -365,16 +380,16 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[kE], const typename 
 #pragma unroll
         for (int m = 0; m < (1 << R); ++m) ar.settle(v[(b << R) | m]);
       }
-      if (is_mid<R>(b, i)) mid();
+      if (is_mid<R, LE>(b, i)) mid();
     }
   }
 }
 
 // Inverse radix-2^R pass over gap bits [LO, LO+R): stages l = LO .. LO+R-1.
-template <int LOGN, int LO, int R, class A, class F>
-__device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename A::TW (&w)[pass_twiddles<R>()],
+template <int LOGN, int LO, int R, class A, class F, int E>
+__device__ __forceinline__ void inv_pass(typename A::T (&v)[E], const typename A::TW (&w)[pass_twiddles<R, ilog2(E)>()],
                                          const A& ar, const NttPrime& pr, F&& mid) {
-  constexpr int SUB = kE >> R;
+  constexpr int LE = ilog2(E), SUB = E >> R;
   int n = 0;
 #pragma unroll
   for (int b = 0; b < SUB; ++b) {
@@ -396,7 +411,7 @@ __device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename 
 #pragma unroll
         for (int m = 0; m < (1 << R); ++m) ar.settle(v[(b << R) | m]);
       }
-      if (is_mid<R>(b, i)) mid();
+      if (is_mid<R, LE>(b, i)) mid();
     }
   }
 }
@@ -406,22 +421,23 @@ __device__ __forceinline__ void inv_pass(typename A::T (&v)[kE], const typename 
 // region: LDS operations of one wave execute in order, so only a compiler
 // barrier is needed.  Otherwise the whole workgroup synchronises before (other
 // waves may still read their regions), between, and after.
-template <int LOGN, bool INV, int P, class T>
-__device__ __forceinline__ void exchange(T (&v)[kE], T* lds, unsigned t) {
-  using A = PassMap<LOGN, INV, P>;
-  using B = PassMap<LOGN, INV, P + 1>;
-  constexpr bool in_wave = A::WAVE_LO == B::WAVE_LO || Passes<LOGN>::WAVE_BITS == 0;
+template <int LOGN, bool INV, int P, class T, int E>
+__device__ __forceinline__ void exchange(T (&v)[E], T* lds, unsigned t) {
+  constexpr int LE = ilog2(E);
+  using A = PassMap<LOGN, INV, P, LE>;
+  using B = PassMap<LOGN, INV, P + 1, LE>;
+  constexpr bool in_wave = A::WAVE_LO == B::WAVE_LO || Passes<LOGN, LE>::WAVE_BITS == 0;
   if constexpr (!in_wave) __syncthreads();
   T* wbase = lds + lds_pos(A::elem(t, 0));
 #pragma unroll
-  for (int j = 0; j < kE; ++j) wbase[A::slot_offset(j)] = v[j];
+  for (int j = 0; j < (1 << LE); ++j) wbase[A::slot_offset(j)] = v[j];
   if constexpr (in_wave)
     __builtin_amdgcn_wave_barrier();
   else
     __syncthreads();
   const T* rbase = lds + lds_pos(B::elem(t, 0));
 #pragma unroll
-  for (int j = 0; j < kE; ++j) v[j] = rbase[B::slot_offset(j)];
+  for (int j = 0; j < (1 << LE); ++j) v[j] = rbase[B::slot_offset(j)];
   if constexpr (in_wave)
     __builtin_amdgcn_wave_barrier();
   else
@@ -480,21 +496,21 @@ __device__ __forceinline__ void ntt_regs(typename A::T (&v)[kE], typename A::T* 
 }
 
 // Register layouts at the boundaries of a transform.
-template <int LOGN>
-__device__ __forceinline__ unsigned fwd_in_index(unsigned t, int j) { return PassMap<LOGN, false, 0>::elem(t, j); }
-template <int LOGN>
+template <int LOGN, int LE = kLogE>
+__device__ __forceinline__ unsigned fwd_in_index(unsigned t, int j) { return PassMap<LOGN, false, 0, LE>::elem(t, j); }
+template <int LOGN, int LE = kLogE>
 __device__ __forceinline__ unsigned fwd_out_index(unsigned t, int j) {
-  return PassMap<LOGN, false, Passes<LOGN>::NP - 1>::elem(t, j);
+  return PassMap<LOGN, false, Passes<LOGN, LE>::NP - 1, LE>::elem(t, j);
 }
-template <int LOGN>
-__device__ __forceinline__ unsigned inv_in_index(unsigned t, int j) { return PassMap<LOGN, true, 0>::elem(t, j); }
-template <int LOGN>
+template <int LOGN, int LE = kLogE>
+__device__ __forceinline__ unsigned inv_in_index(unsigned t, int j) { return PassMap<LOGN, true, 0, LE>::elem(t, j); }
+template <int LOGN, int LE = kLogE>
 __device__ __forceinline__ unsigned inv_out_index(unsigned t, int j) {
-  return PassMap<LOGN, true, Passes<LOGN>::NP - 1>::elem(t, j);
+  return PassMap<LOGN, true, Passes<LOGN, LE>::NP - 1, LE>::elem(t, j);
 }
 
-template <int LOGN>
-constexpr int ntt_threads() { return (1 << LOGN) >> kLogE; }
+template <int LOGN, int LE = kLogE>
+constexpr int ntt_threads() { return (1 << LOGN) >> LE; }
 
 constexpr size_t lds_bytes(int log_n) { return (((size_t)1 << log_n) + ((size_t)1 << log_n) / 16) * 8; }
 
