@@ -194,12 +194,16 @@ __device__ __forceinline__ void digit_factors(uint64_t (&y)[D][kE], const KsRows
   }
 }
 
-// Targets per column-forward thread: the digit factors y are computed once
-// for G targets (all six float-path data primes at L = 6: c1 is then read
-// once per digit, instead of once per target group on different XCDs).
-template <class A>
+// Targets per column-forward thread: the digit's column is read and its
+// factors y computed once for G targets (all six float-path data primes at
+// L = 6: c1 is then read once per digit, instead of once per target group on
+// different XCDs).  On the integer path one-prime digits take every key
+// prime (their stores then overlap the next target's stages: 123 -> 103 us
+// at dnum = 6, batch 64); larger digits one target, since their factors
+// would not fit the registers beside a second target's values.
+template <class A, int D>
 constexpr unsigned kColTargets() {
-  return std::is_same<typename A::T, double>::value ? 6u : 1u;
+  return std::is_same<typename A::T, double>::value ? 6u : (D == 1 ? 7u : 1u);
 }
 
 // x mod q_t for a canonical residue x of another key prime: one conditional
@@ -287,8 +291,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColFw
 template <int D, class AU>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1 ? 3 : 2)))
     ks_cols_fwd_both(KsRows f, unsigned t_u64, unsigned n_u64, unsigned nu) {
-  if (blockIdx.x < nu) cols_fwd_body<D, AU, 1>(f, t_u64, n_u64, blockIdx.x);
-  else cols_fwd_body<D, ArF64Lean, kColTargets<ArF64Lean>()>(f, 0u, t_u64, blockIdx.x - nu);
+  if (blockIdx.x < nu) cols_fwd_body<D, AU, kColTargets<AU, D>()>(f, t_u64, n_u64, blockIdx.x);
+  else cols_fwd_body<D, ArF64Lean, kColTargets<ArF64Lean, D>()>(f, 0u, t_u64, blockIdx.x - nu);
 }
 
 // ------------------------------------------------------------------ phase B
@@ -622,7 +626,7 @@ static int uniform_digit(const KsConst& kc) {
 template <int D, class AU>
 static void launch_cols_fwd(const KsRows& f, unsigned dnum, unsigned t_u64, unsigned K, hipStream_t s) {
   const auto grid = [&](unsigned t_n, unsigned g) { return dim3((f.cts * dnum * ((t_n + g - 1) / g) * kCols + 255) / 256); };
-  constexpr unsigned GU = kColTargets<ArU64>(), GF = kColTargets<ArF64Lean>();
+  constexpr unsigned GU = kColTargets<ArU64, D>(), GF = kColTargets<ArF64Lean, D>();
   if (!t_u64) {  // every prime on the integer path
     hipLaunchKernelGGL((ks_cols_fwd_kernel<D, AU, GU>), grid(K, GU), dim3(256), 0, s, f, 0u, K);
     return;

@@ -1,7 +1,8 @@
 // CPU check of the integer helpers in modarith.hpp against 128-bit host
 // arithmetic: shoup_quotient(w, m) == floor(w 2^64 / q) and mul_shoup /
 // mul_barrett == a w mod q, for primes from 2^20 to 2^62 and edge operands
-// (0, 1, q-1, q/2, random).  Plants one wrong ratio to show the check fails.
+// (0, 1, q-1, q/2, random), and mul_mont (x k 2^-64 mod q) for primes below
+// 2^60.  Plants a wrong ratio and a wrong -q^-1 to show the checks fail.
 #include <cstdio>
 #include <random>
 #include <vector>
@@ -31,6 +32,23 @@ static int check(uint64_t q, std::mt19937_64& rng, const Barrett m) {
   return bad;
 }
 
+// mul_mont(x, k) for the lazy integer key products: x below 12q (a forward
+// transform's output bound), k canonical, q < 2^60.  The result must lie in
+// [0, 2q) and satisfy r 2^64 == x k (mod q).
+static int check_mont(uint64_t q, uint64_t nq, std::mt19937_64& rng) {
+  int bad = 0;
+  const uint64_t x12 = 12 * q;
+  std::vector<uint64_t> xs = {0, 1, q - 1, q, 2 * q + 1, x12 - 1, x12 / 2};
+  std::vector<uint64_t> ks = {0, 1, q - 1, q / 2};
+  for (int i = 0; i < 400; ++i) xs.push_back(rng() % x12), ks.push_back(rng() % q);
+  for (uint64_t x : xs)
+    for (size_t j = 0; j < ks.size(); j += (x < 8 ? 1 : 37)) {
+      const uint64_t k = ks[j], r = mul_mont(x, k, q, nq);
+      if (r >= 2 * q || (((u128)r << 64) % q) != ((u128)x * k) % q) ++bad;
+    }
+  return bad;
+}
+
 int main() {
   std::mt19937_64 rng(12345);
   const std::vector<uint64_t> primes = {
@@ -45,7 +63,20 @@ int main() {
   Barrett wrong = ratio(primes[2]);
   wrong.r0 -= 1ull << 40;
   const int planted = check(primes[2], rng, wrong);
-  printf("bad=%d planted=%d\n", bad, planted);
-  printf(bad == 0 && planted > 0 ? "ALL OK\n" : "FAIL\n");
-  return !(bad == 0 && planted > 0);
+  // Montgomery products on the primes below 2^60; -q^-1 mod 2^64 by Newton
+  // iteration (each step doubles the correct low bits), pinned by q nq == -1
+  int mont_bad = 0, mont_planted = 0;
+  for (uint64_t q : primes) {
+    if (q >> 60) continue;
+    uint64_t y = q;  // q q == 1 mod 8: three correct bits
+    for (int i = 0; i < 6; ++i) y *= 2 - q * y;
+    const uint64_t nq = 0 - y;
+    if (q * nq != ~0ull) ++mont_bad;
+    mont_bad += check_mont(q, nq, rng);
+    mont_planted += check_mont(q, nq + 2, rng) > 0;
+  }
+  printf("bad=%d planted=%d mont_bad=%d mont_planted=%d\n", bad, planted, mont_bad, mont_planted);
+  const bool ok = bad == 0 && planted > 0 && mont_bad == 0 && mont_planted == 4;
+  printf(ok ? "ALL OK\n" : "FAIL\n");
+  return !ok;
 }

@@ -1,5 +1,6 @@
 // CPU check of the NTT register/LDS layout (PassMap in ntt_core.hpp), for every
-// pass of every transform size:
+// pass of every transform size with 16 coefficients per thread, and of the
+// 1024-coefficient row transforms with 8 and 4 coefficients per thread:
 //   - elem(t, j) is a bijection onto [0, N);
 //   - lds_pos(elem(t, j)) == lds_pos(elem(t, 0)) + slot_offset(j), inside the
 //     N + N/16 padded buffer;
@@ -14,10 +15,11 @@
 #include "ntt_core.hpp"
 using namespace praghip;
 
-template <int LOGN, bool INV, int P>
+template <int LOGN, bool INV, int P, int LE = kLogE>
 int check_pass() {
-  using M = PassMap<LOGN, INV, P>;
-  constexpr unsigned N = 1u << LOGN, THREADS = N >> kLogE, LIMIT = N + N / 16;
+  using M = PassMap<LOGN, INV, P, LE>;
+  constexpr int kE = 1 << LE;
+  constexpr unsigned N = 1u << LOGN, THREADS = N >> LE, LIMIT = N + N / 16;
   std::vector<int> seen(N, 0);
   int bad = 0;
   for (unsigned t = 0; t < THREADS; ++t)
@@ -34,8 +36,8 @@ int check_pass() {
     for (unsigned t = 0; t < THREADS; ++t)
       for (int b = 0; b < (kE >> M::R); ++b)
         if ((M::elem(t, b << M::R) >> (M::LO + M::R)) != (M::elem(t & ~63u, b << M::R) >> (M::LO + M::R))) ++bad;
-  if constexpr (P + 1 < Passes<LOGN>::NP) {
-    using B = PassMap<LOGN, INV, P + 1>;
+  if constexpr (P + 1 < Passes<LOGN, LE>::NP) {
+    using B = PassMap<LOGN, INV, P + 1, LE>;
     if (M::WAVE_LO == B::WAVE_LO)
       for (unsigned t = 0; t < THREADS; ++t) {
         const unsigned w = t >> 6;
@@ -48,28 +50,29 @@ int check_pass() {
           if (!found) ++bad;
         }
       }
-    bad += check_pass<LOGN, INV, P + 1>();
+    bad += check_pass<LOGN, INV, P + 1, LE>();
   }
-  if (bad) printf("LOGN=%d INV=%d pass=%d: %d violations\n", LOGN, int(INV), P, bad);
+  if (bad) printf("LOGN=%d LE=%d INV=%d pass=%d: %d violations\n", LOGN, LE, int(INV), P, bad);
   return bad;
 }
 
-template <int LOGN>
+template <int LOGN, int LE = kLogE>
 int check_size() {
   // after the last forward pass registers 2k and 2k + 1 sit at adjacent,
   // 16-byte aligned positions (the keyswitch loads its keys in pairs)
-  using Last = PassMap<LOGN, false, Passes<LOGN>::NP - 1>;
+  using Last = PassMap<LOGN, false, Passes<LOGN, LE>::NP - 1, LE>;
   int bad = 0;
-  for (unsigned t = 0; t < (1u << LOGN) >> kLogE; ++t)
-    for (int j = 0; j < kE; j += 2) bad += (Last::elem(t, j) & 1) || Last::elem(t, j + 1) != Last::elem(t, j) + 1;
-  if (bad) printf("LOGN=%d: %d unpaired forward outputs\n", LOGN, bad);
-  return bad + check_pass<LOGN, false, 0>() + check_pass<LOGN, true, 0>();
+  for (unsigned t = 0; t < (1u << LOGN) >> LE; ++t)
+    for (int j = 0; j < (1 << LE); j += 2)
+      bad += (Last::elem(t, j) & 1) || Last::elem(t, j + 1) != Last::elem(t, j) + 1;
+  if (bad) printf("LOGN=%d LE=%d: %d unpaired forward outputs\n", LOGN, LE, bad);
+  return bad + check_pass<LOGN, false, 0, LE>() + check_pass<LOGN, true, 0, LE>();
 }
 
 int main() {
   const int bad = check_size<4>() + check_size<5>() + check_size<6>() + check_size<7>() + check_size<8>() +
                   check_size<9>() + check_size<10>() + check_size<11>() + check_size<12>() + check_size<13>() +
-                  check_size<14>();
+                  check_size<14>() + check_size<10, 3>() + check_size<10, 2>();
   printf(bad ? "FAIL\n" : "ALL OK\n");
   return bad != 0;
 }
