@@ -301,7 +301,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1
 // exchange crossing the two waves, the others within a wave): forward stages
 // 4-13 of each digit's row, the key products summed over the digits in
 // registers, inverse stages 0-9 of both sums.  Eight coefficients per lane
-// keep a wave within 168 VGPRs, so a SIMD holds three waves.
+// keep a wave within 168 VGPRs, so a SIMD holds three waves.  The row's
+// forward twiddles are staged in LDS once per item (16 KiB beside the 8.5 KiB
+// exchange buffer: six items fit a CU's 160 KiB), so the digits' passes issue
+// no vector-memory loads, and the next digit's row and this digit's key words
+// are in flight while the passes run (vector loads complete in order: a
+// twiddle load behind them would wait for them).
 constexpr int kRowLE = 3;                           // 8 coefficients per lane
 constexpr unsigned kRow2Threads = 1u << (kRowLog - kRowLE);  // 128: the item's two waves
 
@@ -354,6 +359,66 @@ __device__ __forceinline__ void row_passes_e(typename A::T (&v)[E], typename A::
   }
 }
 
+// The forward twiddles of one row in LDS: stage s (4 <= s < 14) of the N =
+// 16384 transform has 2^(s-4) groups inside a row, the table entries
+// (1 << s) + (row << (s - 4)) + k; they sit at [2^(s-4) - 1, 2^(s-3) - 1),
+// 1023 entries in all.  An item loads them once, with its 128 threads, and
+// every digit's forward passes read them there, so no vector-memory load
+// stands between a digit's row and key loads and their use.
+constexpr unsigned kRowTw = (1u << kRowLog) - 1;
+constexpr int kRowKeyPass = 3;
+
+template <class TW>
+__device__ __forceinline__ void row_twiddles_fill(TW* ltw, const TW* __restrict__ tab, unsigned row, unsigned t2) {
+#pragma unroll
+  for (unsigned i = 0; i < (kRowTw + kRow2Threads - 1) / kRow2Threads; ++i) {
+    const unsigned e = t2 + i * kRow2Threads;
+    if (e < kRowTw) {
+      const unsigned m = e + 1, sl = 31u - unsigned(__builtin_clz(m));  // s - 4
+      ltw[e] = tab[(1u << (sl + 4)) + (row << sl) + (m - (1u << sl))];
+    }
+  }
+}
+
+// Twiddles of forward row pass P from the row's LDS copy: the group index
+// inside the row is local >> (LO + R).
+template <int P, int LE, class TW>
+__device__ __forceinline__ void row_twiddles_lds(TW (&w)[(pass_tw_count<kRowLog, false, P, LE>())], unsigned t,
+                                                 const TW* ltw) {
+  using M = PassMap<kRowLog, false, P, LE>;
+  constexpr int LO = M::LO, R = M::R, SUB = (1 << LE) >> R;
+  int n = 0;
+#pragma unroll
+  for (int b = 0; b < SUB; ++b) {
+    const unsigned hi_lane = M::elem(t, b << R) >> (LO + R);
+    const unsigned hi = M::uniform_groups() ? __builtin_amdgcn_readfirstlane(hi_lane) : hi_lane;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int sl = kRowLog - LO - R + i;
+#pragma unroll
+      for (int k = 0; k < (1 << i); ++k) w[n++] = ltw[(1u << sl) - 1 + (hi << i) + k];
+    }
+  }
+}
+
+// Forward passes P .. NP - 1 of a row, twiddles from LDS; at_kp() runs at
+// the start of pass KP (the item issues its key loads there).
+template <int P, int KP, class A, int E, class F>
+__device__ __forceinline__ void row_passes_fwd_lds(typename A::T (&v)[E], typename A::T* lds, unsigned t,
+                                                   const typename A::TW* ltw, const A& ar, F&& at_kp) {
+  constexpr int LE = ilog2(E);
+  using S = Passes<kRowLog, LE>;
+  constexpr int LO = S::lo(false, P), R = S::r(false, P);
+  if constexpr (P == KP) at_kp();
+  typename A::TW w[pass_tw_count<kRowLog, false, P, LE>()];
+  row_twiddles_lds<P, LE>(w, t, ltw);
+  fwd_pass<kLog, LO, R>(v, w, ar, [] {});
+  if constexpr (P + 1 < S::NP) {
+    exchange<kRowLog, false, P>(v, lds, t);
+    row_passes_fwd_lds<P + 1, KP>(v, lds, t, ltw, ar, at_kp);
+  }
+}
+
 // Item (ciphertext bl, prime t, row) on the two waves of the workgroup
 // (thread t2 < 128).  Policy A:
 //   ArU64L    - every key prime below 2^60: Montgomery key products x k 2^-64
@@ -368,7 +433,7 @@ __device__ __forceinline__ void row_passes_e(typename A::T (&v)[E], typename A::
 //   ArF64Lean - the float data primes (q < 2^50), exact FP64 products.
 template <class A>
 __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, unsigned bl, unsigned t,
-                                          unsigned row, unsigned t2, typename A::T* lds) {
+                                          unsigned row, unsigned t2, typename A::T* lds, typename A::TW* ltw) {
   using T = typename A::T;
   constexpr int E = 1 << kRowLE;
   constexpr bool kF64 = std::is_same<T, double>::value;
@@ -377,29 +442,49 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
   const unsigned b = f.b0 + bl;
   const NttPrime pr = f.primes[t];
   const A ar(pr);
-  const typename A::TW* tf = fwd_table<A>(f, int(t));
   const typename A::TW* ti = inv_table<A>(f, int(t));
   const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
+  const uint64_t* e0 = f.e + (size_t(bl) * dnum * K + t) * kN + (row << kRowLog);
+  const size_t e_step = size_t(K) * kN;  // digit to digit in E
+  // the row's forward twiddles into LDS, then the first digit's row (the
+  // twiddle loads are issued first, so their wait before the LDS writes
+  // leaves the row's loads in flight)
+  row_twiddles_fill(ltw, fwd_table<A>(f, int(t)), row, t2);
+  uint64_t en[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) en[k] = e0[fwd_in_index<kRowLog, kRowLE>(t2, k)];
+  __syncthreads();
   T a0[E], a1[E];
   if constexpr (kMont) {
 #pragma unroll
     for (int k = 0; k < E; ++k) a0[k] = a1[k] = 0;
   }
   for (unsigned j = 0; j < dnum; ++j) {
-    const uint64_t* src = f.e + ((size_t(bl) * dnum + j) * K + t) * kN + (row << kRowLog);
     T v[E];
 #pragma unroll
-    for (int k = 0; k < E; ++k) v[k] = load_form<A>(src[fwd_in_index<kRowLog, kRowLE>(t2, k)]);
-    row_passes_e<false, 0>(v, lds, t2, row, tf, ar, pr);
+    for (int k = 0; k < E; ++k) v[k] = load_form<A>(en[k]);
+    if (j + 1 < dnum) {  // the next digit's row, in flight during this digit's passes
+      const uint64_t* src = e0 + (j + 1) * e_step;
+#pragma unroll
+      for (int k = 0; k < E; ++k) en[k] = src[fwd_in_index<kRowLog, kRowLE>(t2, k)];
+    }
+    // the digit's key words, issued at the start of forward pass kRowKeyPass:
+    // registers r, r + 1 hold adjacent coefficients after the last forward
+    // pass, so one 16-byte load per key limb and pair
     const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << kLog);
     const uint64_t* k1 = k0 + (size_t(K) << kLog);
+    ulonglong2 kav[E / 2], kkv[E / 2];
+    row_passes_fwd_lds<0, kRowKeyPass>(v, lds, t2, ltw, ar, [&] {
+#pragma unroll
+      for (int r = 0; r < E; r += 2) {
+        const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog, kRowLE>(t2, r);
+        kav[r / 2] = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+        kkv[r / 2] = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+      }
+    });
 #pragma unroll
     for (int r = 0; r < E; r += 2) {
-      // registers r, r + 1 hold adjacent coefficients after the last forward
-      // pass: one 16-byte load per key limb
-      const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog, kRowLE>(t2, r);
-      const ulonglong2 ka = *reinterpret_cast<const ulonglong2*>(k0 + pos);
-      const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+      const ulonglong2 ka = kav[r / 2], kk = kkv[r / 2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int rr = r + h;
@@ -462,6 +547,7 @@ template <class AU>
 __global__ void __launch_bounds__(kRow2Threads) __attribute__((amdgpu_waves_per_eu(3)))
     ks_rows2_kernel(KsRows f, unsigned t_u64) {
   __shared__ __attribute__((aligned(16))) uint64_t lds[kRowLds];
+  __shared__ ulonglong2 ltw[kRowTw];  // the row's forward twiddles (doubles on the float path)
   const KsConst& kc = *f.kc;
   const unsigned K = unsigned(kc.K);
   const unsigned item = blockIdx.x, t2 = threadIdx.x;
@@ -470,11 +556,11 @@ __global__ void __launch_bounds__(kRow2Threads) __attribute__((amdgpu_waves_per_
   if (item >= f.cts * K * rows) return;
   if (item < u64_items) {
     const unsigned row = item % rows, t = t_u64 + (item / rows) % n_u64, bl = item / (rows * n_u64);
-    row_item2<AU>(f, kc, bl, t, row, t2, lds);
+    row_item2<AU>(f, kc, bl, t, row, t2, lds, ltw);
   } else {
     const unsigned x = item - u64_items;
     const unsigned row = x % rows, t = (x / rows) % t_u64, bl = x / (rows * t_u64);
-    row_item2<ArF64Lean>(f, kc, bl, t, row, t2, reinterpret_cast<double*>(lds));
+    row_item2<ArF64Lean>(f, kc, bl, t, row, t2, reinterpret_cast<double*>(lds), reinterpret_cast<double*>(ltw));
   }
 }
 
