@@ -52,8 +52,11 @@ hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint6
 // once per column group, instead of once per column.  A weight word meets up
 // to kMacLimbs inputs, so it gets a Shoup quotient (from the Barrett ratio)
 // and the products are Shoup products: exact, like the reference's Barrett-128
-// products, with fewer 64-bit multiplies.
+// products, with fewer 64-bit multiplies.  LAZY (every prime below 2^60): the
+// products are left in [0, 2q) and the sums reduced by 8q after every fourth
+// block, so they stay below 16q < 2^64, and made canonical once at the end.
 constexpr int kMacCoords = 4, kMacLimbs = 8;
+template <bool LAZY>
 __global__ void __launch_bounds__(256)
     token_mac_kernel(const uint64_t* __restrict__ in, const uint64_t* __restrict__ w, uint64_t* __restrict__ out,
                      size_t coords, size_t blocks, size_t limbs, int log_n, BarrettList bl) {
@@ -83,8 +86,21 @@ __global__ void __launch_bounds__(256)
           const uint64_t wq = shoup_quotient(wv, m);
 #pragma unroll
           for (int k = 0; k < kMacLimbs; ++k) {
-            const uint64_t v = acc[c][k] + mul_shoup(x[k], wv, wq, m.q);
-            acc[c][k] = v >= m.q ? v - m.q : v;
+            if constexpr (LAZY) {
+              acc[c][k] += mul_shoup_lazy(x[k], wv, wq, m.q);
+            } else {
+              const uint64_t v = acc[c][k] + mul_shoup(x[k], wv, wq, m.q);
+              acc[c][k] = v >= m.q ? v - m.q : v;
+            }
+          }
+        }
+        if constexpr (LAZY) {
+          if ((b & 3) == 3) {
+            const uint64_t q8 = 8 * m.q;
+#pragma unroll
+            for (int c = 0; c < kMacCoords; ++c)
+#pragma unroll
+              for (int k = 0; k < kMacLimbs; ++k) acc[c][k] = acc[c][k] >= q8 ? acc[c][k] - q8 : acc[c][k];
           }
         }
       }
@@ -94,7 +110,14 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int k = 0; k < kMacLimbs; ++k) {
           const size_t l = l0 + size_t(k) * P;
-          if (l < limbs) out[(c0 + c) * words + (l << log_n) + z] = acc[c][k];
+          uint64_t v = acc[c][k];
+          if constexpr (LAZY) {  // below 16q -> [0, q)
+            v = v >= 8 * m.q ? v - 8 * m.q : v;
+            v = v >= 4 * m.q ? v - 4 * m.q : v;
+            v = v >= 2 * m.q ? v - 2 * m.q : v;
+            v = v >= m.q ? v - m.q : v;
+          }
+          if (l < limbs) out[(c0 + c) * words + (l << log_n) + z] = v;
         }
       }
     }
@@ -106,9 +129,15 @@ hipError_t launch_token_mac(const uint64_t* in, const uint64_t* w, uint64_t* out
   BarrettList bl{};
   for (int i = 0; i < primes; ++i) bl.m[i] = m[i];
   bl.count = primes;
+  bool lazy = true;
+  for (int i = 0; i < primes; ++i) lazy = lazy && m[i].q < (1ull << 60);
   const size_t total = ((coords + kMacCoords - 1) / kMacCoords * size_t(primes)) << log_n;
-  hipLaunchKernelGGL(token_mac_kernel, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks, limbs,
-                     log_n, bl);
+  if (lazy)
+    hipLaunchKernelGGL(token_mac_kernel<true>, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks,
+                       limbs, log_n, bl);
+  else
+    hipLaunchKernelGGL(token_mac_kernel<false>, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks,
+                       limbs, log_n, bl);
   return hipGetLastError();
 }
 
