@@ -103,15 +103,19 @@ def test_enc0(gpu, primes):
         z.evaluate(samples)
 
 
-@pytest.mark.parametrize("log_n,blocks,groups", [(14, 3, 5), (12, 2, 9)])
-def test_matrix_batch(gpu, log_n, blocks, groups):
+@pytest.mark.parametrize("log_n,blocks,groups,primes",
+                         [(14, 3, 5, "locked"), (12, 2, 9, "50bit"), (12, 5, 4, "50bit"), (12, 5, 6, "62bit")])
+def test_matrix_batch(gpu, log_n, blocks, groups, primes):
     """evaluate_device_batch: `groups` evaluations in one call against the
     per-evaluation entry point and the oracle (ragged last group of the
-    4-column product tiles)."""
+    4-column product tiles).  Every prime below 2^60: the column product's
+    lazy sums (five blocks: a reduction by 8q after the fourth); primes up to
+    2^62: a reduction per product."""
     import torch
-    print(f"[matrix-batch] log_n={log_n} blocks={blocks} groups={groups}", flush=True)
+    print(f"[matrix-batch] log_n={log_n} blocks={blocks} groups={groups} {primes}", flush=True)
     n = 1 << log_n
-    q = cf.LOCKED_PRIMES[:6] if log_n == 14 else cf.primes_below(50, 2 * n, 6)
+    q = {"locked": cf.LOCKED_PRIMES[:6], "50bit": cf.primes_below(50, 2 * n, 6),
+         "62bit": cf.primes_below(62, 2 * n, 6)}[primes]
     ct = oracle.fill_residues(blocks * 2 * 6, n, q, 500 + blocks).reshape(blocks, 2, 6, n)
     rings = oracle.fill_u64(groups * blocks * n, 501).reshape(groups, blocks, n) & np.uint64(T59)
     rings[-1, 0, :3] = [T59, 0, 1 << 58]
