@@ -220,6 +220,7 @@ int build_ntt_host(const uint64_t* q, size_t P, unsigned log_n, const uint64_t* 
     const uint64_t last = mulmod(w_last, invn[0], qq);
     pr.last = last;
     pr.last_q = shoup_q(last, qq);
+    pr.one_q = shoup_q(1, qq);
     pr.use_f64 = qq < (1ull << 50);
     pr.qd = double(qq);
     pr.qinv = 1.0 / double(qq);

@@ -111,6 +111,12 @@ hipError_t launch_ring_sum_rows(const uint64_t* a, uint64_t* out, size_t rows, s
                                 hipStream_t s);
 hipError_t launch_lift59(const uint64_t* ring, uint64_t* out, size_t blocks, int log_n, size_t width,
                          const PrimeList& q, hipStream_t s);
+// Forward NTT of lifted ring words: limb l = b P + k of out is the lift of ring
+// block b (lift59_residue mod q_k = pl.q[k], the layout of launch_lift59's
+// width), then transformed; one pass over memory when every prime is on the
+// integer path.
+hipError_t launch_ntt_lift(const uint64_t* ring, size_t width, uint64_t* out, size_t blocks, const PrimeList& pl,
+                           const NttDevice& d, hipStream_t s);
 hipError_t launch_dyadic_mac(const uint64_t* a, const uint64_t* w, uint64_t* out, size_t blocks, size_t limbs,
                              int log_n, size_t w_limbs, const Barrett* m, int primes, hipStream_t s);
 hipError_t launch_local_dot_scale(const uint64_t* shares, const uint64_t* weights, size_t words, size_t slots,

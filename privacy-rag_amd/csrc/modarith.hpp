@@ -93,6 +93,17 @@ PH_HD uint64_t shoup_quotient(uint64_t w, const Barrett m) {
   return rem >= m.q ? t + 1 : t;
 }
 
+// The signed value of a ring-2^59 word v (bit 58 the sign) as a canonical
+// residue mod q (resident.cu:23-30, matrix.cu:23-26): v + ((q - 2^59) &
+// -(v >> 58)) for the reference's primes (q > 2^59); the remainder for smaller
+// primes.
+PH_HD uint64_t lift59_residue(uint64_t v, uint64_t q) {
+  if (q > (1ull << 59)) return v + ((q - (1ull << 59)) & (0ull - (v >> 58)));
+  if (!(v >> 58)) return v % q;
+  const uint64_t d = ((1ull << 59) - v) % q;
+  return d ? q - d : 0;
+}
+
 // -------------------------------------------------------------------- float
 struct ShoupF {
   double w, wq;  // operand (exact integer), operand / q

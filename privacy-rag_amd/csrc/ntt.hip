@@ -20,15 +20,53 @@ namespace praghip {
 // the last pass and the stores instead of starting after them; the other
 // kernels have no registers to spare for them and load each limb at the top
 // of its turn.
-template <int LOGN, bool INV, class A>
+//
+// LIFT (forward only): limb l = b P + k is not read from data but formed on
+// load from ring block b, lift59_residue mod q_k (ring[b][z] when width = 0;
+// ring[b][width-1-z] for z < width and 0 above otherwise), so the lifted limbs
+// never pass through memory.
+struct NttLift {
+  const uint64_t* ring = nullptr;
+  size_t width = 0;
+};
+
+template <int LOGN, bool INV, class A, bool LIFT = false>
 __global__ void __launch_bounds__(ntt_threads<LOGN>())
     ntt_kernel(uint64_t* __restrict__ data, size_t count, const NttPrime* __restrict__ primes,
-               const typename A::TW* __restrict__ tw, int P, const int* __restrict__ sel, int C) {
+               const typename A::TW* __restrict__ tw, int P, const int* __restrict__ sel, int C, NttLift lift) {
   __shared__ __attribute__((aligned(16))) uint64_t lds[(1 << LOGN) + (1 << LOGN) / 16];
   using T = typename A::T;
   const unsigned t = threadIdx.x;
   const auto limb_of = [&](size_t v) { return (v / unsigned(C)) * unsigned(P) + unsigned(sel[v % unsigned(C)]); };
   const auto in_index = [&](int j) { return INV ? inv_in_index<LOGN>(t, j) : fwd_in_index<LOGN>(t, j); };
+  // the input words of limb `limb` in the first pass's register layout (with
+  // LIFT the ring words, lifted by `lifted` once the limb's turn comes)
+  const auto load = [&](uint64_t (&raw)[kE], size_t limb) {
+    if constexpr (LIFT) {
+      // coefficient z reads base[sign * z]: base = ring[b] (sign +1), or the
+      // last word of the token block ring[b][width - 1] (sign -1, z < width)
+      const size_t b = limb / unsigned(P);
+      const bool rev = lift.width != 0;
+      const uint64_t* base = lift.ring + (rev ? b * lift.width + lift.width - 1 : b << LOGN);
+      const long long sign = rev ? -1 : 1;
+      const unsigned limit = rev ? unsigned(lift.width) : (1u << LOGN);
+#pragma unroll
+      for (int j = 0; j < kE; ++j) {
+        const unsigned z = in_index(j);
+        raw[j] = z < limit ? base[sign * (long long)z] : 0;
+      }
+    } else {
+      const uint64_t* x = data + (limb << LOGN);
+#pragma unroll
+      for (int j = 0; j < kE; ++j) raw[j] = x[in_index(j)];
+    }
+  };
+  const auto lifted = [&](uint64_t v, const NttPrime& pr) {
+    if constexpr (LIFT)
+      return lift59_residue(v, pr);
+    else
+      return v;
+  };
   const auto store = [&](const A& ar, T (&x)[kE], size_t limb) {
     uint64_t* out = data + (limb << LOGN);
     if (!INV) {
@@ -45,11 +83,7 @@ __global__ void __launch_bounds__(ntt_threads<LOGN>())
     size_t v = blockIdx.x;
     if (v >= count) return;
     uint64_t raw[kE];
-    {
-      const uint64_t* x = data + (limb_of(v) << LOGN);
-#pragma unroll
-      for (int j = 0; j < kE; ++j) raw[j] = x[in_index(j)];
-    }
+    load(raw, limb_of(v));
     for (; v < count; v += gridDim.x) {
       const size_t limb = limb_of(v);
       const int p = int(limb % unsigned(P));
@@ -57,14 +91,10 @@ __global__ void __launch_bounds__(ntt_threads<LOGN>())
       const A ar(pr);
       T x[kE];
 #pragma unroll
-      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(raw[j]);
+      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(lifted(raw[j], pr));
       const size_t vn = v + gridDim.x;
       ntt_regs<LOGN, INV>(x, reinterpret_cast<T*>(lds), t, tw + (size_t(p) << LOGN), ar, pr, [&] {
-        if (vn < count) {
-          const uint64_t* xn = data + (limb_of(vn) << LOGN);
-#pragma unroll
-          for (int j = 0; j < kE; ++j) raw[j] = xn[in_index(j)];
-        }
+        if (vn < count) load(raw, limb_of(vn));
       });
       store(ar, x, limb);
     }
@@ -74,10 +104,11 @@ __global__ void __launch_bounds__(ntt_threads<LOGN>())
       const int p = int(limb % unsigned(P));
       const NttPrime pr = primes[p];
       const A ar(pr);
-      const uint64_t* xv = data + (limb << LOGN);
+      uint64_t raw[kE];
+      load(raw, limb);
       T x[kE];
 #pragma unroll
-      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(xv[in_index(j)]);
+      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(lifted(raw[j], pr));
       ntt_regs<LOGN, INV>(x, reinterpret_cast<T*>(lds), t, tw + (size_t(p) << LOGN), ar, pr);
       store(ar, x, limb);
     }
@@ -85,7 +116,7 @@ __global__ void __launch_bounds__(ntt_threads<LOGN>())
 }
 
 // Resident workgroups per CU times the CU count, cached per kernel.
-template <int LOGN, bool INV, class A>
+template <int LOGN, bool INV, class A, bool LIFT>
 static unsigned persistent_grid() {
   static unsigned grid = 0;
   if (!grid) {
@@ -93,7 +124,7 @@ static unsigned persistent_grid() {
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ntt_kernel<LOGN, INV, A>, ntt_threads<LOGN>(), 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ntt_kernel<LOGN, INV, A, LIFT>, ntt_threads<LOGN>(), 0) !=
             hipSuccess ||
         per_cu < 1)
       per_cu = 1;
@@ -110,15 +141,16 @@ static size_t subset_count(size_t limbs, int P, const int* host_sel, int C) {
   return count;
 }
 
-template <int LOGN, bool INV, class A>
+template <int LOGN, bool INV, class A, bool LIFT = false>
 static hipError_t launch_subset(uint64_t* data, size_t limbs, const NttDevice& d, const typename A::TW* tw,
-                                const int* sel_dev, const int* sel_host, int C, hipStream_t s) {
+                                const int* sel_dev, const int* sel_host, int C, hipStream_t s, NttLift lift = {}) {
   if (!C) return hipSuccess;
   const size_t count = subset_count(limbs, d.P, sel_host, C);
   if (!count) return hipSuccess;
   const dim3 block{unsigned(ntt_threads<LOGN>())};
-  const dim3 grid{unsigned(std::min<size_t>(count, persistent_grid<LOGN, INV, A>()))};
-  hipLaunchKernelGGL((ntt_kernel<LOGN, INV, A>), grid, block, 0, s, data, count, d.primes, tw, d.P, sel_dev, C);
+  const dim3 grid{unsigned(std::min<size_t>(count, persistent_grid<LOGN, INV, A, LIFT>()))};
+  hipLaunchKernelGGL((ntt_kernel<LOGN, INV, A, LIFT>), grid, block, 0, s, data, count, d.primes, tw, d.P, sel_dev, C,
+                     lift);
   return hipGetLastError();
 }
 
@@ -143,6 +175,44 @@ static hipError_t launch_ntt_n(bool inverse, uint64_t* data, size_t limbs, const
     e = launch_subset<LOGN, false, ArF64>(data, limbs, d, d.tw_fwd_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
   if (e == hipSuccess && d.n_u64) e = d.lazy_u64 ? u64(TypeTag<ArU64L>{}, inverse) : u64(TypeTag<ArU64>{}, inverse);
   return e;
+}
+
+template <int LOGN>
+static hipError_t launch_ntt_lift_n(const uint64_t* ring, size_t width, uint64_t* out, size_t limbs,
+                                    const NttDevice& d, hipStream_t s) {
+  const NttLift lift{ring, width};
+  return d.lazy_u64 ? launch_subset<LOGN, false, ArU64L, true>(out, limbs, d, d.tw_fwd_u, d.sel_u64, d.host_sel_u64,
+                                                               d.n_u64, s, lift)
+                    : launch_subset<LOGN, false, ArU64, true>(out, limbs, d, d.tw_fwd_u, d.sel_u64, d.host_sel_u64,
+                                                              d.n_u64, s, lift);
+}
+
+// Every prime on the integer path: the lift is done by the transform's loads.
+// With float-path primes (whose kernel has no registers left for the lift's
+// arithmetic) the lift kernel writes the limbs first and the transform runs
+// in place.
+hipError_t launch_ntt_lift(const uint64_t* ring, size_t width, uint64_t* out, size_t blocks, const PrimeList& pl,
+                           const NttDevice& d, hipStream_t s) {
+  const size_t limbs = blocks * size_t(d.P);
+  if (limbs == 0) return hipSuccess;
+  if (d.n_f64) {
+    const hipError_t e = launch_lift59(ring, out, blocks, d.log_n, width, pl, s);
+    return e == hipSuccess ? launch_ntt(false, out, limbs, d, s) : e;
+  }
+  switch (d.log_n) {
+    case 4: return launch_ntt_lift_n<4>(ring, width, out, limbs, d, s);
+    case 5: return launch_ntt_lift_n<5>(ring, width, out, limbs, d, s);
+    case 6: return launch_ntt_lift_n<6>(ring, width, out, limbs, d, s);
+    case 7: return launch_ntt_lift_n<7>(ring, width, out, limbs, d, s);
+    case 8: return launch_ntt_lift_n<8>(ring, width, out, limbs, d, s);
+    case 9: return launch_ntt_lift_n<9>(ring, width, out, limbs, d, s);
+    case 10: return launch_ntt_lift_n<10>(ring, width, out, limbs, d, s);
+    case 11: return launch_ntt_lift_n<11>(ring, width, out, limbs, d, s);
+    case 12: return launch_ntt_lift_n<12>(ring, width, out, limbs, d, s);
+    case 13: return launch_ntt_lift_n<13>(ring, width, out, limbs, d, s);
+    case 14: return launch_ntt_lift_n<14>(ring, width, out, limbs, d, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_ntt(bool inverse, uint64_t* data, size_t limbs, const NttDevice& d, hipStream_t s) {

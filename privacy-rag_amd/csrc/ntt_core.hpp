@@ -37,9 +37,19 @@ struct NttPrime {
   uint64_t last, last_q;      // w_last * N^-1 (Shoup pair), w_last = inv[N-1]
   double qd, qinv;            // q and 1/q as doubles (float path)
   double ninv_f, last_f;      // N^-1 and w_last * N^-1 as doubles
+  uint64_t one_q;             // floor(2^64 / q), the Shoup quotient of 1
   int use_f64;                // q < 2^50: the float path is exact
   int pad;
 };
+
+// lift59_residue with the prime's Shoup quotient of 1 instead of a division
+// (for q <= 2^59: |v| < 2^58 reduced by one Shoup product by 1).
+__host__ __device__ __forceinline__ uint64_t lift59_residue(uint64_t v, const NttPrime& p) {
+  if (p.q > (1ull << 59)) return v + ((p.q - (1ull << 59)) & (0ull - (v >> 58)));
+  const bool neg = (v >> 58) != 0;
+  const uint64_t r = mul_shoup(neg ? (1ull << 59) - v : v, 1, p.one_q, p.q);
+  return neg && r ? p.q - r : r;
+}
 
 __host__ __device__ __forceinline__ unsigned lds_pos(unsigned x) { return x + (x >> 4); }
 

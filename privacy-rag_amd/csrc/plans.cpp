@@ -43,15 +43,17 @@ int matrix_failure(praghip_matrix_plan* p, hipError_t e, const char* what) {
   p->release();
   return fail(PRAGHIP_E_DEVICE, std::string("E_MATRIX_HIP: ") + what + ": " + hipGetErrorString(e));
 }
-// lift -> NTT -> sum of products -> INTT, all on the plan's device buffers
-hipError_t matrix_run(praghip_matrix_plan* p, const uint64_t* ring_dev, uint64_t* out_dev, hipStream_t s) {
+PrimeList host_primes(const praghip_matrix_plan* p) {
   PrimeList pl{};
   for (size_t i = 0; i < p->P; ++i) pl.q[i] = p->host_q[i];
   pl.count = int(p->P);
+  return pl;
+}
+// lift + NTT (one pass) -> sum of products -> INTT, all on the plan's device buffers
+hipError_t matrix_run(praghip_matrix_plan* p, const uint64_t* ring_dev, uint64_t* out_dev, hipStream_t s) {
   Barrett m[kMaxKeyPrimes];
   for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
-  hipError_t e = launch_lift59(ring_dev, p->weight, p->blocks, int(p->log_n), 0, pl, s);
-  if (e == hipSuccess) e = launch_ntt(false, p->weight, p->blocks * p->P, p->d, s);
+  hipError_t e = launch_ntt_lift(ring_dev, 0, p->weight, p->blocks, host_primes(p), p->d, s);
   if (e == hipSuccess)
     e = launch_dyadic_mac(p->input, p->weight, out_dev, p->blocks, 2 * p->P, int(p->log_n), p->P, m, int(p->P), s);
   if (e == hipSuccess) e = launch_ntt(true, out_dev, 2 * p->P, p->d, s);
@@ -185,16 +187,12 @@ static int matrix_batch(praghip_matrix_plan* p, const uint64_t* rings, uint64_t*
   if ((reinterpret_cast<uintptr_t>(rings) | reinterpret_cast<uintptr_t>(output) |
        reinterpret_cast<uintptr_t>(selected)) & 15)
     return fail(PRAGHIP_E_ARGUMENT, "MATRIX_GPU_ALIGNMENT");
-  PrimeList pl{};
-  for (size_t i = 0; i < p->P; ++i) pl.q[i] = p->host_q[i];
-  pl.count = int(p->P);
   Barrett m[kMaxKeyPrimes];
   for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
   const hipStream_t s = pick(stream);
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
-  if (e == hipSuccess) e = launch_lift59(rings, p->bweight, groups * p->blocks, int(p->log_n), 0, pl, s);
-  if (e == hipSuccess) e = launch_ntt(false, p->bweight, groups * p->blocks * p->P, p->d, s);
+  if (e == hipSuccess) e = launch_ntt_lift(rings, 0, p->bweight, groups * p->blocks, host_primes(p), p->d, s);
   if (e == hipSuccess)
     e = launch_token_mac(p->input, p->bweight, output, groups, p->blocks, 2 * p->P, int(p->log_n), m, int(p->P), s);
   if (e == hipSuccess) e = launch_ntt(true, output, groups * 2 * p->P, p->d, s);
@@ -744,13 +742,12 @@ PrimeList token_primes(const praghip_token_plan* p) {
   pl.count = int(p->P);
   return pl;
 }
-// lift -> NTT -> sum over blocks -> (INTT) into p->output
+// lift + NTT (one pass) -> sum over blocks -> (INTT) into p->output
 hipError_t token_product(praghip_token_plan* p, const uint64_t* ring_dev, bool inverse, hipStream_t s) {
   Barrett m[kMaxKeyPrimes];
   for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
   const size_t limbs = p->slots * 2 * p->P;
-  hipError_t e = launch_lift59(ring_dev, p->weight, p->blocks, int(p->log_n), p->width, token_primes(p), s);
-  if (e == hipSuccess) e = launch_ntt(false, p->weight, p->blocks * p->P, p->d, s);
+  hipError_t e = launch_ntt_lift(ring_dev, p->width, p->weight, p->blocks, token_primes(p), p->d, s);
   if (e == hipSuccess)
     e = launch_dyadic_mac(p->input, p->weight, p->output, p->blocks, limbs, int(p->log_n), p->P, m, int(p->P), s);
   if (e == hipSuccess && inverse) e = launch_ntt(true, p->output, limbs, p->d, s);
@@ -1020,8 +1017,7 @@ int praghip_token_evaluate_device_batch(praghip_token_plan* p, const uint64_t* r
   const PrimeList pl = token_primes(p);
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
-  if (e == hipSuccess) e = launch_lift59(rings, p->bweight, coords * p->blocks, int(p->log_n), p->width, pl, s);
-  if (e == hipSuccess) e = launch_ntt(false, p->bweight, coords * p->blocks * p->P, p->d, s);
+  if (e == hipSuccess) e = launch_ntt_lift(rings, p->width, p->bweight, coords * p->blocks, pl, p->d, s);
   if (e == hipSuccess)
     e = launch_token_mac(p->input, p->bweight, p->boutput, coords, p->blocks, limbs, int(p->log_n), m, int(p->P), s);
   if (e == hipSuccess) e = launch_ntt(true, p->boutput, coords * limbs, p->d, s);

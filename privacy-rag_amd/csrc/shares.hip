@@ -93,11 +93,12 @@ hipError_t launch_ring_sum_rows(const uint64_t* a, uint64_t* out, size_t rows, s
 }
 
 // ---------------------------------------------------------------------- lift
-// out[b][k][z] = the signed value of the ring-2^59 word v as a canonical
-// residue mod q_k: v + ((q_k - 2^59) & -(v >> 58)) for the reference's primes
-// (q_k > 2^59), the remainder for smaller primes.  width = 0: v = ring[b][z] over all
-// N coefficients (matrix.cu:23-26).  width > 0: the resident token layout
-// (resident.cu:23-30), v = ring[b][width-1-z] for z < width, 0 above.
+// out[b][k][z] = lift59_residue(v, q_k), the signed value of the ring-2^59 word
+// v as a canonical residue mod q_k.  width = 0: v = ring[b][z] over all N
+// coefficients (matrix.cu:23-26).  width > 0: the resident token layout
+// (resident.cu:23-30), v = ring[b][width-1-z] for z < width, 0 above.  The
+// plans fuse this into the forward NTT's loads (launch_ntt_lift); this kernel
+// serves praghip_lift59.
 __global__ void lift59_kernel(const uint64_t* __restrict__ ring, uint64_t* __restrict__ out, size_t blocks,
                               int log_n, size_t width, PrimeList q) {
   const size_t n = size_t(1) << log_n, P = size_t(q.count), total = blocks * P * n;
@@ -113,15 +114,7 @@ __global__ void lift59_kernel(const uint64_t* __restrict__ ring, uint64_t* __res
       out[i] = 0;
       continue;
     }
-    const uint64_t qk = q.q[k];
-    if (qk > (1ull << 59)) {
-      out[i] = v + ((qk - (1ull << 59)) & (0ull - (v >> 58)));
-    } else if (!(v >> 58)) {
-      out[i] = v % qk;
-    } else {
-      const uint64_t d = ((1ull << 59) - v) % qk;
-      out[i] = d ? qk - d : 0;
-    }
+    out[i] = lift59_residue(v, q.q[k]);
   }
 }
 
