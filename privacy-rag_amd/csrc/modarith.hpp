@@ -39,6 +39,82 @@ struct Shoup {
 PH_HD uint64_t mul_shoup_lazy(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
   return a * w - mulhi64(a, wq) * q;
 }
+
+// The same product with fewer VALU instructions on gfx950, for the
+// transforms' butterflies.  The compiler's expansion of
+// a 64-bit high word spends four of its nine instructions on moves that build
+// zero-extended register pairs.  Here, from 32-bit halves:
+//   m1 = a1 b0 + hi(a0 b0) < 2^64,
+//   a0 b1 + m1 = c 2^64 + m2      (v_mad_u64_u32 reports the carry c in an
+//                                  SGPR pair),
+//   hi(a b) = a1 b1 + (m2 >> 32) + c 2^32,
+// where a1 b1 + (m2 >> 32) < 2^64 and adding the carry to the high half cannot
+// overflow: six instructions.  UNI: b is the same in every lane of the wave
+// and was loaded into scalar registers by a scalar memory load (the carry
+// product reads its high half from an SGPR); otherwise it is read from VGPRs,
+// which is correct for any b.  The empty asm statements keep an assembled
+// 64-bit result as one register pair, so that later additions do not split it
+// into zero-extended halves again.
+//
+// gfx950 needs two wait states between a VALU write of an SGPR lane mask (the
+// carry) and a VALU read of it as a carry-in.  The compiler inserts them for
+// its own instructions but cannot see this dependency between two asm
+// statements: the high-word product that must come between them is one, the
+// s_nop 0 before the v_addc the other.  A UNI operand must not come from a
+// VALU write (v_readfirstlane), whose hazard the compiler would not cover
+// either.
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ __forceinline__ uint64_t pin_pair(uint64_t x) {
+  asm("" : "+v"(x));
+  return x;
+}
+template <bool UNI>
+__device__ __forceinline__ uint64_t mad_carry(uint32_t a0, uint32_t b1, uint64_t m1, uint64_t& c) {
+  uint64_t m2;
+  if constexpr (UNI)
+    asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=v"(m2), "=s"(c) : "v"(a0), "s"(b1), "v"(m1));
+  else
+    asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=v"(m2), "=s"(c) : "v"(a0), "v"(b1), "v"(m1));
+  return m2;
+}
+// a1 b1 + (m2 >> 32) + c 2^32
+__device__ __forceinline__ uint64_t mulhi_top(uint32_t a1, uint32_t b1, uint64_t m2, uint64_t c) {
+  const uint64_t r = uint64_t(a1) * b1 + uint32_t(m2 >> 32);
+  uint32_t rh;
+  uint64_t c_out;
+  asm("s_nop 0\n\tv_addc_co_u32_e64 %0, %1, %2, 0, %3" : "=v"(rh), "=s"(c_out) : "v"(uint32_t(r >> 32)), "s"(c));
+  return pin_pair((uint64_t(rh) << 32) | uint32_t(r));
+}
+#endif
+template <bool UNI>
+PH_HD uint64_t mulhi64_t(uint64_t a, uint64_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t a0 = uint32_t(a), a1 = uint32_t(a >> 32), b0 = uint32_t(b), b1 = uint32_t(b >> 32);
+  uint64_t c;
+  const uint64_t m2 = mad_carry<UNI>(a0, b1, uint64_t(a1) * b0 + __umulhi(a0, b0), c);
+  return mulhi_top(a1, b1, m2, c);
+#else
+  return mulhi64(a, b);
+#endif
+}
+
+// mul_shoup_lazy with the quotient from mulhi64_t<UNI> (UNI: w and wq are the
+// same in every lane).  The low word a w - Q q = a w + Q (2^64 - q) mod 2^64
+// is one sum: the two low 32x32 products in a 64-bit accumulator, the four
+// cross products added to its high half.
+template <bool UNI>
+PH_HD uint64_t mul_shoup_lazy_t(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint64_t Q = mulhi64_t<UNI>(a, wq), nq = 0 - q;
+  const uint32_t a0 = uint32_t(a), a1 = uint32_t(a >> 32), w0 = uint32_t(w), w1 = uint32_t(w >> 32);
+  const uint32_t Q0 = uint32_t(Q), Q1 = uint32_t(Q >> 32), n0 = uint32_t(nq), n1 = uint32_t(nq >> 32);
+  const uint64_t x = uint64_t(Q0) * n0 + uint64_t(a0) * w0;
+  const uint32_t h = uint32_t(x >> 32) + a0 * w1 + a1 * w0 + Q0 * n1 + Q1 * n0;
+  return pin_pair((uint64_t(h) << 32) | uint32_t(x));
+#else
+  return mul_shoup_lazy(a, w, wq, q);
+#endif
+}
 PH_HD uint64_t mul_shoup(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
   uint64_t r = mul_shoup_lazy(a, w, wq, q);
   return r >= q ? r - q : r;

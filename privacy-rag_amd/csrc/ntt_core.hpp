@@ -100,24 +100,28 @@ struct ArU64 {
     return x >= q ? x - q : x;
   }
   __device__ __forceinline__ uint64_t to_u64_inv(T x) const { return x >= q ? x - q : x; }  // [0,2q)
+  // UNI: the twiddle is the same in every lane and held in scalar registers
+  template <bool UNI = false>
   __device__ __forceinline__ void fwd(T& x, T& y, TW w) const {  // CT, values in [0,4q)
     T a = x >= q2 ? x - q2 : x;
-    const T t = mul_shoup_lazy(y, w.x, w.y, q);
+    const T t = mul_shoup_lazy_t<UNI>(y, w.x, w.y, q);
     x = a + t;
     y = a - t + q2;
   }
-  __device__ __forceinline__ void fwd_at(int, T& x, T& y, TW w) const { fwd(x, y, w); }
+  template <bool UNI = false>
+  __device__ __forceinline__ void fwd_at(int, T& x, T& y, TW w) const { fwd<UNI>(x, y, w); }
+  template <bool UNI = false>
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {  // GS, values in [0,2q)
     T s = x + y;
     s = s >= q2 ? s - q2 : s;
     const T d = x - y + q2;
     x = s;
-    y = mul_shoup_lazy(d, w.x, w.y, q);
+    y = mul_shoup_lazy_t<UNI>(d, w.x, w.y, q);
   }
   __device__ __forceinline__ void inv_last(T& x, T& y, const NttPrime& p) const {
     const T s = x + y, d = x - y + q2;
-    x = mul_shoup_lazy(s, p.ninv, p.ninv_q, q);
-    y = mul_shoup_lazy(d, p.last, p.last_q, q);
+    x = mul_shoup_lazy_t<false>(s, p.ninv, p.ninv_q, q);
+    y = mul_shoup_lazy_t<false>(d, p.last, p.last_q, q);
   }
   __device__ __forceinline__ void settle(T&) const {}
   // Harvey's bounds hold without re-centring
@@ -144,24 +148,26 @@ struct ArU64L : ArU64 {
     x = x >= q2 ? x - q2 : x;
     return x >= q ? x - q : x;
   }
+  template <bool UNI = false>
   __device__ __forceinline__ void fwd_at(int s, T& x, T& y, TW w) const {
     T a = x;
     if (s > 0 && s % 4 == 0) a = a >= q8 ? a - q8 : a;
-    const T t = mul_shoup_lazy(y, w.x, w.y, q);
+    const T t = mul_shoup_lazy_t<UNI>(y, w.x, w.y, q);
     x = a + t;
     y = a - t + q2;
   }
+  template <bool UNI = false>
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
     T s = x + y;
     s = s >= q4 ? s - q4 : s;
     const T d = x - y + q4;
     x = s;
-    y = mul_shoup_lazy(d, w.x, w.y, q);
+    y = mul_shoup_lazy_t<UNI>(d, w.x, w.y, q);
   }
   __device__ __forceinline__ void inv_last(T& x, T& y, const NttPrime& p) const {
     const T s = x + y, d = x - y + q4;
-    x = mul_shoup_lazy(s, p.ninv, p.ninv_q, q);
-    y = mul_shoup_lazy(d, p.last, p.last_q, q);
+    x = mul_shoup_lazy_t<false>(s, p.ninv, p.ninv_q, q);
+    y = mul_shoup_lazy_t<false>(d, p.last, p.last_q, q);
   }
 };
 
@@ -194,13 +200,16 @@ struct ArF64 {
   __device__ __forceinline__ uint64_t to_u64_fwd(T x) const { return to_u64(x); }
   __device__ __forceinline__ uint64_t to_u64_inv(T x) const { return to_u64(x); }
   __device__ __forceinline__ T mul(T a, TW w) const { return mul_f64(a, w, w * qinv, q); }
+  template <bool = false>
   __device__ __forceinline__ void fwd(T& x, T& y, TW w) const {
     const T t = mul(y, w);
     const T a = x;
     x = a + t;
     y = a - t;
   }
+  template <bool = false>
   __device__ __forceinline__ void fwd_at(int, T& x, T& y, TW w) const { fwd(x, y, w); }
+  template <bool = false>
   __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
     const T s = x + y, d = x - y;
     x = s;
@@ -368,7 +377,8 @@ __device__ __forceinline__ constexpr bool is_mid(int b, int i) {
   return ((1 << LE) >> R) == 1 ? (i == R / 2 - 1) : (b == ((1 << LE) >> R) / 2 - 1 && i == R - 1);
 }
 
-template <int LOGN, int LO, int R, class A, class F, int E>
+// UNI: every twiddle of the pass is wave-uniform and in scalar registers.
+template <int LOGN, int LO, int R, bool UNI = false, class A, class F, int E>
 __device__ __forceinline__ void fwd_pass(typename A::T (&v)[E], const typename A::TW (&w)[pass_twiddles<R, ilog2(E)>()],
                                          const A& ar, F&& mid) {
   constexpr int LE = ilog2(E), SUB = E >> R;
@@ -383,7 +393,7 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[E], const typename A
 #pragma unroll
         for (int m = 0; m < (1 << g); ++m) {
           const int j0 = (b << R) | (k << (g + 1)) | m, j1 = j0 | (1 << g);
-          ar.fwd_at(s, v[j0], v[j1], w[n]);
+          ar.template fwd_at<UNI>(s, v[j0], v[j1], w[n]);
         }
       }
       if (A::settle_fwd(s) && s != LOGN - 1) {  // the final stage is reduced on output
@@ -396,7 +406,7 @@ __device__ __forceinline__ void fwd_pass(typename A::T (&v)[E], const typename A
 }
 
 // Inverse radix-2^R pass over gap bits [LO, LO+R): stages l = LO .. LO+R-1.
-template <int LOGN, int LO, int R, class A, class F, int E>
+template <int LOGN, int LO, int R, bool UNI = false, class A, class F, int E>
 __device__ __forceinline__ void inv_pass(typename A::T (&v)[E], const typename A::TW (&w)[pass_twiddles<R, ilog2(E)>()],
                                          const A& ar, const NttPrime& pr, F&& mid) {
   constexpr int LE = ilog2(E), SUB = E >> R;
@@ -414,7 +424,7 @@ __device__ __forceinline__ void inv_pass(typename A::T (&v)[E], const typename A
           if (l == LOGN - 1)  // last stage: one group, twiddle and N^-1 folded
             ar.inv_last(v[j0], v[j1], pr);
           else
-            ar.inv(v[j0], v[j1], w[n]);
+            ar.template inv<UNI>(v[j0], v[j1], w[n]);
         }
       }
       if (A::settle_inv(l) && l != LOGN - 1) {
@@ -466,6 +476,9 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
                                            F&& before_last) {
   using S = Passes<LOGN>;
   constexpr int LO = S::lo(INV, P), R = S::r(INV, P);
+  // uniform groups: the pass's twiddles were loaded by scalar memory loads
+  // (load_invariant at a wave-uniform index)
+  constexpr bool UNI = PassMap<LOGN, INV, P>::uniform_groups();
   if constexpr (P + 1 < S::NP) {
     constexpr int R1 = S::r(INV, P + 1);
     typename A::TW wn[pass_twiddles<R1>()];
@@ -473,18 +486,18 @@ __device__ __forceinline__ void run_passes(typename A::T (&v)[kE], typename A::T
       if constexpr (A::kAhead) load_pass_twiddles<LOGN, INV, P + 1>(wn, t, tab);
     };
     if constexpr (INV)
-      inv_pass<LOGN, LO, R>(v, w, ar, pr, prefetch);
+      inv_pass<LOGN, LO, R, UNI>(v, w, ar, pr, prefetch);
     else
-      fwd_pass<LOGN, LO, R>(v, w, ar, prefetch);
+      fwd_pass<LOGN, LO, R, UNI>(v, w, ar, prefetch);
     exchange<LOGN, INV, P>(v, lds, t);
     if constexpr (!A::kAhead) load_pass_twiddles<LOGN, INV, P + 1>(wn, t, tab);
     run_passes<LOGN, INV, P + 1>(v, lds, t, tab, ar, pr, wn, before_last);
   } else {
     before_last();
     if constexpr (INV)
-      inv_pass<LOGN, LO, R>(v, w, ar, pr, [] {});
+      inv_pass<LOGN, LO, R, UNI>(v, w, ar, pr, [] {});
     else
-      fwd_pass<LOGN, LO, R>(v, w, ar, [] {});
+      fwd_pass<LOGN, LO, R, UNI>(v, w, ar, [] {});
   }
 }
 
