@@ -170,9 +170,9 @@ static hipError_t launch_ntt_n(bool inverse, uint64_t* data, size_t limbs, const
   };
   hipError_t e;
   if (inverse)
-    e = launch_subset<LOGN, true, ArF64>(data, limbs, d, d.tw_inv_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
+    e = launch_subset<LOGN, true, ArF64T>(data, limbs, d, d.tw_inv_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
   else
-    e = launch_subset<LOGN, false, ArF64>(data, limbs, d, d.tw_fwd_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
+    e = launch_subset<LOGN, false, ArF64T>(data, limbs, d, d.tw_fwd_f, d.sel_f64, d.host_sel_f64, d.n_f64, s);
   if (e == hipSuccess && d.n_u64) e = d.lazy_u64 ? u64(TypeTag<ArU64L>{}, inverse) : u64(TypeTag<ArU64>{}, inverse);
   return e;
 }

@@ -225,6 +225,26 @@ struct ArF64 {
   static constexpr bool settle_inv(int l) { return l % 3 == 1; }
 };
 
+// The float path of the standalone transform, whose inputs and outputs are
+// canonical: it re-centres only after forward stages s = 3 mod 5 and inverse
+// stages l = 2 mod 4 (2 and 3 re-centrings at N = 16384 instead of 3 and 4).
+// Bounds (|x| <= M q; a product by a factor |a| <= A q is within
+// (1/2 + 3A/8) q for any A, so M -> 1.375 M + 1/2 per forward stage):
+//   forward : canonical inputs, stages 0..3 reach 1.88, 3.08, 4.73, 7.01;
+//             after a re-centring (q/2 + 1) five stages reach 1.19, 2.13,
+//             3.43, 5.22, 7.68 - factors below 5.3 q, values below 7.7 q;
+//   inverse : sums double from q (canonical) or q/2 + 1 (re-centred), so the
+//             values and the differences that become factors stay within
+//             8 q + 16;
+// every value and remainder stays below 2^53 because q < 2^50 - 2 (q odd,
+// prime).  The keyswitch kernels keep ArF64's schedule, whose bounds their
+// phases rely on.
+struct ArF64T : ArF64 {
+  __device__ explicit ArF64T(const NttPrime& p) : ArF64(p) {}
+  static constexpr bool settle_fwd(int s) { return s % 5 == 3; }
+  static constexpr bool settle_inv(int l) { return l % 4 == 2; }
+};
+
 // The float path with each pass's twiddles loaded when the pass starts (for
 // kernels that keep more than the limb in registers).
 struct ArF64Lean : ArF64 {

@@ -5,9 +5,11 @@
 // the same stages, so every intermediate value here equals the GPU's.
 //
 // For every butterfly output the double must be an exact integer congruent to
-// the exact residue (tracked alongside in 128-bit integers), every factor of
-// a product must stay within 4q and every value below 2^53.  The final
-// canonical outputs are compared with the expected transform.
+// the exact residue (tracked alongside in 128-bit integers) and below 2^53.
+// Both re-centring schedules are replayed: ArF64's (the keyswitch kernels;
+// every factor within 4q, every value below 8q) and ArF64T's (the standalone
+// transform; factors and values within 8q + 16).  The final canonical outputs
+// are compared with the expected transform.
 //
 // Input file (little-endian u64): q, log_n, cases, fwd_pairs[N][2],
 // inv_pairs[N][2], invn_pair[2], then per case: input[N], forward[N] (the
@@ -28,9 +30,9 @@ static uint64_t mulmod(uint64_t a, uint64_t b, uint64_t q) { return (uint64_t)((
 struct Checker {
   uint64_t q;
   double qd, qinv;
-  double max_factor = 0, max_value = 0;
+  double max_factor = 0, max_value = 0, factor_lim;
   long bad = 0;
-  explicit Checker(uint64_t q_) : q(q_), qd(double(q_)), qinv(1.0 / double(q_)) {}
+  Checker(uint64_t q_, double lim) : q(q_), qd(double(q_)), qinv(1.0 / double(q_)), factor_lim(lim) {}
   // residue of an integer-valued double
   uint64_t res(double x) {
     if (x != std::rint(x) || std::fabs(x) >= 9007199254740992.0) { ++bad; return 0; }
@@ -39,7 +41,7 @@ struct Checker {
   }
   double mul(double a, double w, uint64_t wi, uint64_t ai) {
     max_factor = std::fmax(max_factor, std::fabs(a) / qd);
-    if (std::fabs(a) > 4.0 * qd) ++bad;
+    if (std::fabs(a) > factor_lim * qd) ++bad;
     const double r = mul_f64(a, w, w * qinv, qd);
     if (res(r) != mulmod(ai, wi, q)) ++bad;
     return r;
@@ -60,12 +62,20 @@ int main(int argc, char** argv) {
   if (std::fread(fwd.data(), 8, 2 * n, f) != 2 * n || std::fread(inv.data(), 8, 2 * n, f) != 2 * n ||
       std::fread(invn.data(), 8, 2, f) != 2)
     return 2;
-  Checker ck(q);
   const uint64_t last_i = mulmod(inv[2 * (n - 1)], invn[0], q);
+  std::vector<std::vector<uint64_t>> ins(cases, std::vector<uint64_t>(n)), expects(cases, std::vector<uint64_t>(n));
+  for (size_t c = 0; c < cases; ++c)
+    if (std::fread(ins[c].data(), 8, n, f) != n || std::fread(expects[c].data(), 8, n, f) != n) return 2;
+  int fails = 0;
+  for (int sparse = 0; sparse < 2; ++sparse) {
+  const auto settle_fwd = [&](int s) { return sparse ? ArF64T::settle_fwd(s) : ArF64::settle_fwd(s); };
+  const auto settle_inv = [&](int l) { return sparse ? ArF64T::settle_inv(l) : ArF64::settle_inv(l); };
+  const double lim = sparse ? 8.0 + 16.0 / double(q) : 4.0, vlim = sparse ? 8.0 + 16.0 / double(q) : 8.0;
+  Checker ck(q, lim);
   long mismatches = 0;
   for (size_t c = 0; c < cases; ++c) {
-    std::vector<uint64_t> in(n), expect(n);
-    if (std::fread(in.data(), 8, n, f) != n || std::fread(expect.data(), 8, n, f) != n) return 2;
+    const std::vector<uint64_t>& in = ins[c];
+    const std::vector<uint64_t>& expect = expects[c];
     // forward: values and exact residues
     std::vector<double> v(n);
     std::vector<uint64_t> e(in);
@@ -90,7 +100,7 @@ int main(int argc, char** argv) {
           if (ck.res(v[j0]) != e[j0] || ck.res(v[j1]) != e[j1]) ++ck.bad;
         }
       }
-      if (ArF64::settle_fwd(s) && s != log_n - 1)
+      if (settle_fwd(s) && s != log_n - 1)
         for (size_t i = 0; i < n; ++i) {
           v[i] = reduce_f64(v[i], ck.qd, ck.qinv);
           if (std::fabs(v[i]) > 0.5 * ck.qd + 1.0 || ck.res(v[i]) != e[i]) ++ck.bad;
@@ -130,7 +140,7 @@ int main(int argc, char** argv) {
         ck.track(v[j1]);
         if (ck.res(v[j0]) != e[j0] || ck.res(v[j1]) != e[j1]) ++ck.bad;
       }
-      if (ArF64::settle_inv(l) && l != log_n - 1)
+      if (settle_inv(l) && l != log_n - 1)
         for (size_t i = 0; i < n; ++i) {
           v[i] = reduce_f64(v[i], ck.qd, ck.qinv);
           if (std::fabs(v[i]) > 0.5 * ck.qd + 1.0 || ck.res(v[i]) != e[i]) ++ck.bad;
@@ -141,9 +151,12 @@ int main(int argc, char** argv) {
       if (uint64_t(r) != in[i]) ++mismatches;
     }
   }
-  std::printf("q=%llu log_n=%d cases=%zu max_factor=%.3f max_value=%.3f bad=%ld mismatches=%ld\n",
-              (unsigned long long)q, log_n, cases, ck.max_factor, ck.max_value, ck.bad, mismatches);
-  if (ck.bad || mismatches || ck.max_factor > 4.0 || ck.max_value >= 8.0) return 1;
+  std::printf("%s q=%llu log_n=%d cases=%zu max_factor=%.3f max_value=%.3f bad=%ld mismatches=%ld\n",
+              sparse ? "ArF64T" : "ArF64", (unsigned long long)q, log_n, cases, ck.max_factor, ck.max_value, ck.bad,
+              mismatches);
+  if (ck.bad || mismatches || ck.max_factor > lim || ck.max_value > vlim) ++fails;
+  }
+  if (fails) return 1;
   std::printf("ALL OK\n");
   return 0;
 }
