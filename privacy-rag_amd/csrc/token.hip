@@ -50,13 +50,15 @@ hipError_t launch_token_finish(const uint64_t* in, const uint64_t* scaled, uint6
 // per (coordinate group, prime p, coefficient z) walks all limbs l = p (mod P)
 // and kMacCoords columns: each weight word is read once and each input word
 // once per column group, instead of once per column.  A weight word meets up
-// to kMacLimbs inputs, so it gets a Shoup quotient (from the Barrett ratio)
+// to KL inputs (KL limb slots per thread: 8 for the token path's slots x 2P
+// limbs, 2 for a single ciphertext's 2P, so no slot multiplies zeros), so it
+// gets a Shoup quotient (from the Barrett ratio)
 // and the products are Shoup products: exact, like the reference's Barrett-128
 // products, with fewer 64-bit multiplies.  LAZY (every prime below 2^60): the
 // products are left in [0, 2q) and the sums reduced by 8q after every fourth
 // block, so they stay below 16q < 2^64, and made canonical once at the end.
-constexpr int kMacCoords = 4, kMacLimbs = 8;
-template <bool LAZY>
+constexpr int kMacCoords = 4;
+template <bool LAZY, int KL>
 __global__ void __launch_bounds__(256)
     token_mac_kernel(const uint64_t* __restrict__ in, const uint64_t* __restrict__ w, uint64_t* __restrict__ out,
                      size_t coords, size_t blocks, size_t limbs, int log_n, BarrettList bl) {
@@ -66,16 +68,16 @@ __global__ void __launch_bounds__(256)
     const size_t z = i & (n - 1), p = (i >> log_n) % P, c0 = ((i >> log_n) / P) * kMacCoords;
     const Barrett m = bl.m[p];
     const size_t cn = coords - c0 < size_t(kMacCoords) ? coords - c0 : size_t(kMacCoords);
-    for (size_t l0 = p; l0 < limbs; l0 += kMacLimbs * P) {
-      uint64_t acc[kMacCoords][kMacLimbs];
+    for (size_t l0 = p; l0 < limbs; l0 += KL * P) {
+      uint64_t acc[kMacCoords][KL];
 #pragma unroll
       for (int c = 0; c < kMacCoords; ++c)
 #pragma unroll
-        for (int k = 0; k < kMacLimbs; ++k) acc[c][k] = 0;
+        for (int k = 0; k < KL; ++k) acc[c][k] = 0;
       for (size_t b = 0; b < blocks; ++b) {
-        uint64_t x[kMacLimbs];
+        uint64_t x[KL];
 #pragma unroll
-        for (int k = 0; k < kMacLimbs; ++k) {
+        for (int k = 0; k < KL; ++k) {
           const size_t l = l0 + size_t(k) * P;
           x[k] = l < limbs ? in[b * words + (l << log_n) + z] : 0;
         }
@@ -85,7 +87,7 @@ __global__ void __launch_bounds__(256)
           const uint64_t wv = w[(c0 + c) * wcol + ((b * P + p) << log_n) + z];
           const uint64_t wq = shoup_quotient(wv, m);
 #pragma unroll
-          for (int k = 0; k < kMacLimbs; ++k) {
+          for (int k = 0; k < KL; ++k) {
             if constexpr (LAZY) {
               acc[c][k] += mul_shoup_lazy(x[k], wv, wq, m.q);
             } else {
@@ -100,7 +102,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
             for (int c = 0; c < kMacCoords; ++c)
 #pragma unroll
-              for (int k = 0; k < kMacLimbs; ++k) acc[c][k] = acc[c][k] >= q8 ? acc[c][k] - q8 : acc[c][k];
+              for (int k = 0; k < KL; ++k) acc[c][k] = acc[c][k] >= q8 ? acc[c][k] - q8 : acc[c][k];
           }
         }
       }
@@ -108,7 +110,7 @@ __global__ void __launch_bounds__(256)
       for (int c = 0; c < kMacCoords; ++c) {
         if (size_t(c) >= cn) break;
 #pragma unroll
-        for (int k = 0; k < kMacLimbs; ++k) {
+        for (int k = 0; k < KL; ++k) {
           const size_t l = l0 + size_t(k) * P;
           uint64_t v = acc[c][k];
           if constexpr (LAZY) {  // below 16q -> [0, q)
@@ -132,12 +134,16 @@ hipError_t launch_token_mac(const uint64_t* in, const uint64_t* w, uint64_t* out
   bool lazy = true;
   for (int i = 0; i < primes; ++i) lazy = lazy && m[i].q < (1ull << 60);
   const size_t total = ((coords + kMacCoords - 1) / kMacCoords * size_t(primes)) << log_n;
+  // limb slots per thread: the limbs of one prime, rounded up to 2, 4 or 8
+  const size_t per = (limbs + size_t(primes) - 1) / size_t(primes);
+  const int kl = per <= 2 ? 2 : (per <= 4 ? 4 : 8);
+  const auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks, limbs, log_n, bl);
+  };
   if (lazy)
-    hipLaunchKernelGGL(token_mac_kernel<true>, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks,
-                       limbs, log_n, bl);
+    kl == 2 ? go(token_mac_kernel<true, 2>) : kl == 4 ? go(token_mac_kernel<true, 4>) : go(token_mac_kernel<true, 8>);
   else
-    hipLaunchKernelGGL(token_mac_kernel<false>, dim3(elem_grid(total)), dim3(256), 0, s, in, w, out, coords, blocks,
-                       limbs, log_n, bl);
+    kl == 2 ? go(token_mac_kernel<false, 2>) : kl == 4 ? go(token_mac_kernel<false, 4>) : go(token_mac_kernel<false, 8>);
   return hipGetLastError();
 }
 
