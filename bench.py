@@ -222,7 +222,7 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
     shape (bfv_token_batch.inc:176-215 with the locked context: N=16384, six
     60-bit primes + special, 19 blocks of 8192 per slot, 4 slots, bound local
     shares): every coordinate's weight column evaluated to a finished batch
-    (lift, NTT, 19-block product, INTT, Delta term, shift; 16 columns per
+    (lift, NTT, 19-block product, INTT, Delta term, shift; 64 columns per
     batched call), then the 9-level
     acyclic packing tree over the tile (511 merges per slot, 2 keyswitches each,
     dnum=6), level by level in batched launches."""
@@ -250,7 +250,7 @@ def bench_token(torch, praghip, steps, warmup, slots=4):
     rings = ((rings & ((1 << 21) - 1)) - (1 << 20)) & ((1 << 59) - 1)  # signed |w| <= 2^20 as ring words
     rings = rings.view(coords, blocks * width)
     nodes = torch.empty((coords, slots * ct_words), dtype=torch.int64, device="cuda")
-    chunk = 16
+    chunk = 64  # 64 x 114 limbs per transform: 28.5 rounds of one limb per CU, a small tail
     tw.reserve(chunk)
 
     def evaluate_all():
