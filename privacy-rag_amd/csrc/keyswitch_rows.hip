@@ -530,11 +530,13 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
     }
   }
   uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
-  row_passes_e<true, 0>(a0, lds, t2, row, ti, ar, pr);
+  // the lazy path's inverse passes with the compiler's Shoup product (ArU64LC)
+  const std::conditional_t<kMont, ArU64LC, A> ari(pr);
+  row_passes_e<true, 0>(a0, lds, t2, row, ti, ari, pr);
 #pragma unroll
   for (int k = 0; k < E; ++k) pb[inv_out_index<kRowLog, kRowLE>(t2, k)] = store_form<A>(a0[k]);
   __syncthreads();  // the second transform's first exchange reuses the LDS
-  row_passes_e<true, 0>(a1, lds, t2, row, ti, ar, pr);
+  row_passes_e<true, 0>(a1, lds, t2, row, ti, ari, pr);
   uint64_t* pc = pb + (size_t(K) << kLog);
 #pragma unroll
   for (int k = 0; k < E; ++k) pc[inv_out_index<kRowLog, kRowLE>(t2, k)] = store_form<A>(a1[k]);

@@ -40,8 +40,8 @@ PH_HD uint64_t mul_shoup_lazy(uint64_t a, uint64_t w, uint64_t wq, uint64_t q) {
   return a * w - mulhi64(a, wq) * q;
 }
 
-// The same product with fewer VALU instructions on gfx950, for the
-// transforms' butterflies.  The compiler's expansion of
+// The same products with fewer VALU instructions on gfx950, for the
+// transforms' butterflies and the Montgomery key products.  The compiler's expansion of
 // a 64-bit high word spends four of its nine instructions on moves that build
 // zero-extended register pairs.  Here, from 32-bit halves:
 //   m1 = a1 b0 + hi(a0 b0) < 2^64,
@@ -95,6 +95,23 @@ PH_HD uint64_t mulhi64_t(uint64_t a, uint64_t b) {
   return mulhi_top(a1, b1, m2, c);
 #else
   return mulhi64(a, b);
+#endif
+}
+
+// Both words of a*b (lo returned, hi in `hi`); on the device the low word
+// shares the partial products of the high one: lo = a0 b0 + (m2 mod 2^32) 2^32.
+PH_HD uint64_t mul_wide(uint64_t a, uint64_t b, uint64_t& hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t a0 = uint32_t(a), a1 = uint32_t(a >> 32), b0 = uint32_t(b), b1 = uint32_t(b >> 32);
+  const uint64_t p = uint64_t(a0) * b0;
+  uint64_t c;
+  const uint64_t m2 = mad_carry<false>(a0, b1, uint64_t(a1) * b0 + uint32_t(p >> 32), c);
+  hi = mulhi_top(a1, b1, m2, c);
+  return pin_pair((m2 << 32) | uint32_t(p));
+#else
+  const unsigned __int128 x = (unsigned __int128)a * b;
+  hi = (uint64_t)(x >> 64);
+  return (uint64_t)x;
 #endif
 }
 
@@ -154,9 +171,10 @@ PH_HD uint64_t mul_barrett(uint64_t a, uint64_t b, const Barrett m) {
 // a multiple of 2^64; its low word cancels the low word of x k with a carry
 // exactly when that low word is non-zero, and (x k + m q) / 2^64 < 2q.
 PH_HD uint64_t mul_mont(uint64_t x, uint64_t k, uint64_t q, uint64_t nq) {
-  const uint64_t lo = x * k, hi = mulhi64(x, k);
+  uint64_t hi;
+  const uint64_t lo = mul_wide(x, k, hi);
   const uint64_t m = lo * nq;
-  return hi + mulhi64(m, q) + uint64_t(lo != 0);
+  return hi + mulhi64_t<false>(m, q) + uint64_t(lo != 0);
 }
 
 // floor(w 2^64 / q) for w < q, from the Barrett ratio R = floor((2^128-1)/q):

@@ -171,6 +171,24 @@ struct ArU64L : ArU64 {
   }
 };
 
+// ArU64L whose inverse butterfly takes the compiler's Shoup product: the
+// keyswitch rows kernel's inverse passes.  With the carry-out product both in
+// those passes and in the kernel's Montgomery key products, every twiddle
+// product of the rows' inverse passes came out wrong on the GPU (each of the
+// two alone was exact, and no hazard or register conflict showed in the
+// compiled code); this split keeps both kernels' tests exact.
+struct ArU64LC : ArU64L {
+  __device__ explicit ArU64LC(const NttPrime& p) : ArU64L(p) {}
+  template <bool = false>
+  __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
+    T s = x + y;
+    s = s >= q4 ? s - q4 : s;
+    const T d = x - y + q4;
+    x = s;
+    y = mul_shoup_lazy(d, w.x, w.y, q);
+  }
+};
+
 // Float path bounds (q < 2^50, |x| <= M q, mul_f64 gives |t| <= (1/2 + 3A/8) q
 // for a factor |a| <= A q, A <= 4; sums must stay below 2^53 = 8 * 2^50):
 //   forward : inputs |x| <= q; stages 0..2 grow the bound 1 -> 1.88 -> 3.08
