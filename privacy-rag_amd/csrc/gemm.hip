@@ -355,10 +355,14 @@ constexpr int kRawRow = kBK * 8;  // bytes of one raw share row per step
 // 16 bytes per lane from global memory straight into LDS at M0 + lane * 16
 // (global_load_lds_dwordx4).  Issued from inline asm, so the compiler adds no
 // wait of its own for it: the caller waits with s_waitcnt vmcnt(0) before any
-// wave reads what was loaded.
+// wave reads what was loaded.  The LDS DMA reads M0 one wait state after the
+// scalar write that sets it (the compiler's own global_load_lds always leaves
+// one instruction there); the compiler cannot see that dependency into the
+// asm, so the asm starts with s_nop 0.
 __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
   const unsigned lds = unsigned(reinterpret_cast<uintptr_t>((void __attribute__((address_space(3)))*)(lds_wave_base)));
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
 }
 
 // Byte offset of share word k of raw row r in a stage buffer.
