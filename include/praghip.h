@@ -68,6 +68,40 @@ typedef struct praghip_timing {
   uint64_t device_bytes, sensitive_bytes;
 } praghip_timing;
 
+/* Switch::Timing (switch.hpp:10): the phases of the last host-buffer keyswitch
+ * (apply / evaluate), from events on the plan's stream between its launches.
+ * At N = 16384 (digits of one to three primes) the keyswitch runs in three
+ * kernel phases, whose boundaries are not the reference's:
+ *   rns_ntt_ms  - ModUp (decompose, base conversion) and forward stages 0-3
+ *                 of every expanded digit limb (the column kernel);
+ *   product_ms  - forward stages 4-13, the key inner product and inverse
+ *                 stages 0-9 of both sums (the row kernel);
+ *   inverse_ms  - inverse stages 10-13 of the special prime's limbs;
+ *   moddown_ms  - inverse stages 10-13 of the data primes' limbs with ModDown.
+ * At other sizes the whole-limb kernel (ModUp, transforms and product) is
+ * product_ms, its ModDown moddown_ms, and rns_ntt_ms = inverse_ms = 0.
+ * setup_upload_ms is the plan's table, constant and key upload at creation.
+ * The phases sum to kernel_ms of praghip_switch_timing. */
+typedef struct praghip_switch_phases {
+  double setup_upload_ms, upload_ms, rns_ntt_ms, product_ms, inverse_ms, moddown_ms, download_ms;
+  uint64_t device_bytes, sensitive_bytes;
+} praghip_switch_phases;
+
+/* TokenWeights::Timing (resident.hpp:11-12): the phases of the last
+ * host-buffer token evaluation (evaluate, evaluate_finished,
+ * evaluate_local_finished).  lift_ms is 0 when every prime is on the integer
+ * path (the transform lifts the ring words in its loads, so that time is in
+ * ntt_ms); ntt_ms is the forward transform of the weight limbs (one kernel,
+ * so there is no per-stage split like ntt_stages_ms); dyadic_ms the product
+ * summed over the blocks; finish_ms the inverse transform, the local dot with
+ * Delta scaling (bound shares) and the shift-and-add (0 for evaluate, which
+ * returns NTT-form products).  initial_input_upload_ms is the creation's
+ * ciphertext upload.  The phases sum to kernel_ms of praghip_token_timing. */
+typedef struct praghip_token_phases {
+  double initial_input_upload_ms, weight_upload_ms, lift_ms, ntt_ms, dyadic_ms, download_ms, finish_ms;
+  uint64_t input_bytes, ring_weight_bytes, ntt_weight_bytes, output_bytes, device_bytes;
+} praghip_token_phases;
+
 const char *praghip_last_error(void);
 int praghip_version(void);
 /* Number of visible gfx950 devices (0 without a GPU; never initialises HIP
@@ -133,11 +167,22 @@ void praghip_ntt_destroy(praghip_ntt_plan *plan);
  * [dnum][2][L+1][N] NTT-form switching key for `element` (NULL: keys are passed
  * per call).  dnum = L reproduces the reference exactly (one prime per digit,
  * no base conversion); dnum < L uses fast base conversion (ModUp).  max_batch
- * sizes the plan's scratch.  L+1 <= 16. */
+ * sizes the plan's scratch.  L+1 <= 16.
+ * The SEAL arrays Switch::initialize(q, f, r, ni, invp, keys) receives
+ * (switch.hpp:24, extracted by keyswitch/seal_adapter.cpp:24-41) may be
+ * passed as they are: fwd_pairs / inv_pairs [L+1][N][2] (root powers and
+ * inverse root powers, operand and quotient), invn_pairs [L+1][2] (N^-1) and
+ * invp_pairs [L][2] (inv_q_last_mod_q: q[L]^-1 mod q_i).  Each may be NULL
+ * (derived from q); when given it is compared with the derived one and a
+ * mismatch returns PRAGHIP_E_CONTEXT "E_NTT_CONTEXT", so a caller's tables
+ * and the keys it built with them are known to agree with the transforms.
+ * Key words (here and in praghip_keyswitch) must be canonical residues mod
+ * their prime. */
 typedef struct praghip_switch_plan praghip_switch_plan;
 int praghip_switch_plan_create(int device, const uint64_t *q, size_t data_primes, uint32_t log_n,
-                               size_t dnum, const uint64_t *key, uint32_t element, size_t max_batch,
-                               praghip_switch_plan **plan);
+                               size_t dnum, const uint64_t *fwd_pairs, const uint64_t *inv_pairs,
+                               const uint64_t *invn_pairs, const uint64_t *invp_pairs, const uint64_t *key,
+                               uint32_t element, size_t max_batch, praghip_switch_plan **plan);
 /* Switch::apply (keyswitch/seal_adapter.cpp:44-52 + switch.cu:113-125): host
  * [2][L][N] coefficient-form ciphertext -> Galois(element) + keyswitch -> host
  * [2][L][N]. */
@@ -150,11 +195,18 @@ int praghip_switch_evaluate(praghip_switch_plan *plan, const uint64_t *input, ui
 /* Batched device keyswitch: in/out device [batch][2][L][N] (8-byte aligned);
  * keys device [dnum][2][L+1][N] per ciphertext at key_stride words apart (0:
  * one shared key; NULL keys: the plan's key), 16-byte aligned with an even
- * key_stride (E_SWITCH_ALIGNMENT).  galois_elt odd, < 2N (1 = plain switch). */
+ * key_stride (E_SWITCH_ALIGNMENT).  galois_elt odd, < 2N (1 = plain switch).
+ * Device key words must be canonical (k < q_t): they are not checked here,
+ * and with every key prime below 2^60 the key products are Montgomery
+ * products whose lazy bounds assume it (a plan's own key is checked at
+ * creation, E_SWITCH_KEY_CANONICAL). */
 int praghip_keyswitch(praghip_switch_plan *plan, const uint64_t *input, uint64_t *output, size_t batch,
                       const uint64_t *keys, size_t key_stride, uint32_t galois_elt, void *stream);
 int praghip_switch_sync(praghip_switch_plan *plan);
 int praghip_switch_timing(const praghip_switch_plan *plan, praghip_timing *out);
+/* Switch::timing (switch.hpp:10, printed by check_switch.cpp:23): per-phase
+ * times of the last host-buffer call (praghip_switch_phases). */
+int praghip_switch_phase_timing(const praghip_switch_plan *plan, praghip_switch_phases *out);
 int praghip_switch_close(praghip_switch_plan *plan, praghip_cleanup *out);
 void praghip_switch_destroy(praghip_switch_plan *plan);
 
@@ -433,6 +485,9 @@ int praghip_token_stack_store_ready(praghip_token_plan *plan, size_t slot, unsig
                                     void *ready);
 int praghip_token_download_ready(praghip_token_plan *plan, const uint64_t *view, void *ready, uint64_t *output);
 int praghip_token_timing(const praghip_token_plan *plan, praghip_timing *out);
+/* TokenWeights::timing (resident.hpp:11-12, resident.cu:165-166,183-184):
+ * per-phase times of the last host-buffer evaluation (praghip_token_phases). */
+int praghip_token_phase_timing(const praghip_token_plan *plan, praghip_token_phases *out);
 int praghip_token_close(praghip_token_plan *plan, praghip_cleanup *out);
 void praghip_token_destroy(praghip_token_plan *plan);
 

@@ -586,11 +586,14 @@ struct praghip_switch_plan {
   unsigned acc_slots = 0;
   size_t inter_cts = 0;
   hipStream_t stream = nullptr;
-  hipEvent_t ev[4] = {};
+  // start, uploaded, the four kernel phases, downloaded
+  static constexpr int kEvents = 7;
+  hipEvent_t ev[kEvents] = {};
   praghip_timing timing{};
+  praghip_switch_phases phases{};
   praghip_cleanup cleanup{};
   bool closing = false;
-  void release() { release_all(device, buf, stream, ev, 4, cleanup, closing); }
+  void release() { release_all(device, buf, stream, ev, kEvents, cleanup, closing); }
   ~praghip_switch_plan() { release(); }
 };
 
@@ -671,7 +674,9 @@ int build_ks_const(const uint64_t* q, size_t L, size_t dnum, unsigned log_n, KsC
 extern "C" {
 
 int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes, uint32_t log_n, size_t dnum,
-                               const uint64_t* key, uint32_t element, size_t max_batch, praghip_switch_plan** plan) {
+                               const uint64_t* fwd_pairs, const uint64_t* inv_pairs, const uint64_t* invn_pairs,
+                               const uint64_t* invp_pairs, const uint64_t* key, uint32_t element, size_t max_batch,
+                               praghip_switch_plan** plan) {
   if (!plan || !q) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   *plan = nullptr;
   const size_t L = data_primes, K = L + 1;
@@ -679,8 +684,16 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
     return fail(PRAGHIP_E_SHAPE, "E_SWITCH_SHAPE");
   uint32_t ginv = 1;
   if (!galois_inverse(element, log_n, ginv)) return fail(PRAGHIP_E_ARGUMENT, "E_SWITCH_ELEMENT");
+  // the caller's SEAL tables (Switch::initialize, switch.hpp:24) are checked
+  // against the ones derived from q
   NttHost h;
-  if (int rc = build_ntt_host(q, K, log_n, nullptr, nullptr, nullptr, h)) return rc;
+  if (int rc = build_ntt_host(q, K, log_n, fwd_pairs, inv_pairs, invn_pairs, h)) return rc;
+  if (invp_pairs)
+    for (size_t i = 0; i < L; ++i) {  // inv_q_last_mod_q (seal_adapter.cpp:40): q[L]^-1 mod q_i, Shoup quotient
+      const uint64_t ip = invmod(q[L] % q[i], q[i]);
+      if (invp_pairs[2 * i] != ip || invp_pairs[2 * i + 1] != shoup_q(ip, q[i]))
+        return fail(PRAGHIP_E_CONTEXT, "E_NTT_CONTEXT: inv_q_last_mod_q is not q[L]^-1 mod q_i");
+    }
   const size_t n = size_t(1) << log_n, key_words = dnum * 2 * K * n;
   if (key)
     for (size_t i = 0; i < key_words; ++i)
@@ -701,11 +714,13 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
   for (auto& ev : p->ev)
     if (e == hipSuccess) e = hipEventCreate(&ev);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[0], p->stream);
   if (e == hipSuccess) e = upload_ntt(h, log_n, p->buf, p->d, p->stream);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->kc_dev, sizeof(KsConst), false);
   if (e == hipSuccess) e = hipMemcpyAsync(p->kc_dev, &p->kc, sizeof(KsConst), hipMemcpyHostToDevice, p->stream);
   if (e == hipSuccess && key) e = p->buf.alloc((void**)&p->key, key_words * 8, true);
   if (e == hipSuccess && key) e = hipMemcpyAsync(p->key, key, key_words * 8, hipMemcpyHostToDevice, p->stream);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[1], p->stream);
   // the fused kernel's running sums and work queue, only for shapes the
   // three-phase kernels do not take (they never touch either)
   const bool fused = !keyswitch_rows_supported(p->kc);
@@ -723,15 +738,21 @@ int praghip_switch_plan_create(int device, const uint64_t* q, size_t data_primes
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->in, 2 * L * n * 8, true);
   if (e == hipSuccess) e = p->buf.alloc((void**)&p->out, 2 * L * n * 8, true);
   if (e == hipSuccess) e = hipStreamSynchronize(p->stream);
+  float setup_ms = 0;
+  if (e == hipSuccess) e = hipEventElapsedTime(&setup_ms, p->ev[0], p->ev[1]);
   if (e != hipSuccess) return switch_failure(p.get(), e, "create");
   p->timing.device_bytes = p->buf.total_bytes();
   p->timing.sensitive_bytes = p->buf.sensitive_bytes();
+  p->phases.setup_upload_ms = setup_ms;
+  p->phases.device_bytes = p->timing.device_bytes;
+  p->phases.sensitive_bytes = p->timing.sensitive_bytes;
   *plan = p.release();
   return PRAGHIP_OK;
 }
 
 static hipError_t keyswitch_chunks(praghip_switch_plan* p, const uint64_t* in, uint64_t* out, size_t batch,
-                                   const uint64_t* keys, size_t key_stride, uint32_t ginv, hipStream_t s) {
+                                   const uint64_t* keys, size_t key_stride, uint32_t ginv, hipStream_t s,
+                                   hipEvent_t* phase_events = nullptr) {
   const size_t n = size_t(1) << p->log_n, ct_words = 2 * p->L * n;
   for (size_t b0 = 0; b0 < batch; b0 += p->max_batch) {
     KsArgs a;
@@ -747,6 +768,7 @@ static hipError_t keyswitch_chunks(praghip_switch_plan* p, const uint64_t* in, u
     a.queue = p->queue;
     a.inter = p->inter;
     a.inter_cts = p->inter_cts;
+    a.phase_events = batch <= p->max_batch ? phase_events : nullptr;
     const hipError_t e = launch_keyswitch(a, p->kc_dev, p->kc, p->d, s);
     if (e != hipSuccess) return e;
   }
@@ -787,25 +809,29 @@ static int switch_host_run(praghip_switch_plan* p, const uint64_t* input, uint64
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
   hipStream_t s = p->stream;
+  // events: 0 start, 1 uploaded, 2..5 after the four kernel phases, 6 downloaded
   if (e == hipSuccess) e = hipEventRecord(p->ev[0], s);
   if (e == hipSuccess) e = hipMemcpyAsync(p->in, input, words * 8, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipEventRecord(p->ev[1], s);
-  if (e == hipSuccess) e = keyswitch_chunks(p, p->in, p->out, 1, p->key, 0, ginv, s);
-  if (e == hipSuccess) e = hipEventRecord(p->ev[2], s);
+  if (e == hipSuccess) e = keyswitch_chunks(p, p->in, p->out, 1, p->key, 0, ginv, s, p->ev + 2);
   if (e == hipSuccess) e = hipMemcpyAsync(output, p->out, words * 8, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipEventRecord(p->ev[3], s);
-  if (e == hipSuccess) e = hipEventSynchronize(p->ev[3]);
-  float t01 = 0, t12 = 0, t23 = 0;
-  if (e == hipSuccess) e = hipEventElapsedTime(&t01, p->ev[0], p->ev[1]);
-  if (e == hipSuccess) e = hipEventElapsedTime(&t12, p->ev[1], p->ev[2]);
-  if (e == hipSuccess) e = hipEventElapsedTime(&t23, p->ev[2], p->ev[3]);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[6], s);
+  if (e == hipSuccess) e = hipEventSynchronize(p->ev[6]);
+  float t[6] = {};
+  for (int i = 0; i < 6 && e == hipSuccess; ++i) e = hipEventElapsedTime(&t[i], p->ev[i], p->ev[i + 1]);
   if (e != hipSuccess) {
     std::memset(output, 0, words * 8);
     return switch_failure(p, e, what);
   }
-  p->timing.upload_ms = t01;
-  p->timing.kernel_ms = t12;
-  p->timing.download_ms = t23;
+  p->timing.upload_ms = t[0];
+  p->timing.kernel_ms = double(t[1]) + t[2] + t[3] + t[4];
+  p->timing.download_ms = t[5];
+  p->phases.upload_ms = t[0];
+  p->phases.rns_ntt_ms = t[1];
+  p->phases.product_ms = t[2];
+  p->phases.inverse_ms = t[3];
+  p->phases.moddown_ms = t[4];
+  p->phases.download_ms = t[5];
   return PRAGHIP_OK;
 }
 
@@ -832,6 +858,12 @@ int praghip_switch_sync(praghip_switch_plan* p) {
 int praghip_switch_timing(const praghip_switch_plan* p, praghip_timing* out) {
   if (!p || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
   *out = p->timing;
+  return PRAGHIP_OK;
+}
+
+int praghip_switch_phase_timing(const praghip_switch_plan* p, praghip_switch_phases* out) {
+  if (!p || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *out = p->phases;
   return PRAGHIP_OK;
 }
 

@@ -66,6 +66,11 @@ struct KsArgs {
   unsigned* queue;       // scratch [kQueueWords], zero before the first launch (the kernel leaves it zero)
   uint64_t* inter = nullptr;  // scratch [inter_cts][dnum][K][N]: expanded digits of the three-phase path
   size_t inter_cts = 0;       // ciphertexts per three-phase chunk (0: whole-limb path only)
+  // four events recorded on the stream after the ModUp + forward columns, the
+  // rows, the special prime's inverse columns and the ModDown columns (the
+  // whole-limb path records the first at its start, the next two after its
+  // kernel); null: none.  Only for a batch of one chunk.
+  hipEvent_t* phase_events = nullptr;
 };
 // Work-queue counters of the fused keyswitch: one ticket per XCD group, then
 // the count of finished workgroups.

@@ -451,10 +451,16 @@ hipError_t launch_keyswitch(const KsArgs& a, const KsConst* kc_dev, const KsCons
   f.xcd = 0;
   hipError_t e = hipErrorInvalidValue;
   const int log_n = kc.log_n;
+  if (a.phase_events) (void)hipEventRecord(a.phase_events[0], s);
   PH_LOGN_SWITCH(e = launch_fused_n<LG>(f, s); break);
   if (e != hipSuccess) return e;
+  if (a.phase_events) {
+    (void)hipEventRecord(a.phase_events[1], s);
+    (void)hipEventRecord(a.phase_events[2], s);
+  }
   hipLaunchKernelGGL(ks_moddown_kernel, dim3(grid_for(a.batch * n)), dim3(256), 0, s, a.prod, a.in, a.out, kc_dev,
                      a.batch, a.galois_inv);
+  if (a.phase_events) (void)hipEventRecord(a.phase_events[3], s);
   return hipGetLastError();
 }
 

@@ -723,11 +723,14 @@ struct praghip_token_plan {
   size_t batch_cap = 0;
   uint64_t *bweight = nullptr, *boutput = nullptr, *bscaled = nullptr, *bpartial = nullptr;
   hipStream_t stream = nullptr;
-  hipEvent_t ev[4] = {};
+  // start, uploaded, lifted, transformed, summed, finished, downloaded
+  static constexpr int kEvents = 7;
+  hipEvent_t ev[kEvents] = {};
   praghip_timing timing{};
+  praghip_token_phases phases{};
   praghip_cleanup cleanup{};
   bool closing = false;
-  void release() { release_all(device, buf, stream, ev, 4, cleanup, closing); }
+  void release() { release_all(device, buf, stream, ev, kEvents, cleanup, closing); }
   ~praghip_token_plan() { release(); }
 };
 
@@ -742,22 +745,35 @@ PrimeList token_primes(const praghip_token_plan* p) {
   pl.count = int(p->P);
   return pl;
 }
-// lift + NTT (one pass) -> sum over blocks -> (INTT) into p->output
-hipError_t token_product(praghip_token_plan* p, const uint64_t* ring_dev, bool inverse, hipStream_t s) {
+// lift + NTT (one pass) -> sum over blocks -> (INTT) into p->output.  ev
+// (null: none) receives events after the lift (ev[0], only when the lift is a
+// kernel of its own, i.e. a prime is on the float path), after the transform
+// (ev[1]) and after the sum (ev[2]).
+hipError_t token_product(praghip_token_plan* p, const uint64_t* ring_dev, bool inverse, hipStream_t s,
+                         hipEvent_t* ev = nullptr) {
   Barrett m[kMaxKeyPrimes];
   for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
   const size_t limbs = p->slots * 2 * p->P;
-  hipError_t e = launch_ntt_lift(ring_dev, p->width, p->weight, p->blocks, token_primes(p), p->d, s);
+  hipError_t e = hipSuccess;
+  if (ev && p->d.n_f64) {  // a float-path prime: the lift is its own kernel, timed apart
+    e = launch_lift59(ring_dev, p->weight, p->blocks, int(p->log_n), p->width, token_primes(p), s);
+    if (e == hipSuccess) e = hipEventRecord(ev[0], s);
+    if (e == hipSuccess) e = launch_ntt(false, p->weight, p->blocks * p->P, p->d, s);
+  } else {
+    e = launch_ntt_lift(ring_dev, p->width, p->weight, p->blocks, token_primes(p), p->d, s);
+  }
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[1], s);
   if (e == hipSuccess)
     e = launch_dyadic_mac(p->input, p->weight, p->output, p->blocks, limbs, int(p->log_n), p->P, m, int(p->P), s);
+  if (e == hipSuccess && ev) e = hipEventRecord(ev[2], s);
   if (e == hipSuccess && inverse) e = launch_ntt(true, p->output, limbs, p->d, s);
   return e;
 }
 // the whole evaluate_device path; residues [slots][P] device, or null for the
 // bound local shares
 hipError_t token_finished(praghip_token_plan* p, const uint64_t* ring_dev, const uint64_t* residues, uint64_t* out,
-                          hipStream_t s) {
-  hipError_t e = token_product(p, ring_dev, true, s);
+                          hipStream_t s, hipEvent_t* ev = nullptr) {
+  hipError_t e = token_product(p, ring_dev, true, s, ev);
   if (e == hipSuccess && !residues) {
     Barrett m[kMaxKeyPrimes];
     for (size_t i = 0; i < p->P; ++i) m[i] = barrett_of(p->host_q[i]);
@@ -793,6 +809,21 @@ void bfv_delta(const std::vector<uint64_t>& q, std::vector<uint64_t>& delta, uin
     for (size_t i = sh.size(); i-- > 0;) acc = ((acc << 64) | sh[i]) % x;
     delta.push_back(uint64_t(acc));
   }
+}
+// Milliseconds between consecutive phase events 0..n of a host-buffer
+// evaluation; without a lift kernel (event 2 not recorded) the lift takes 0
+// and the transform runs from event 1.
+hipError_t token_phase_times(praghip_token_plan* p, float* t, int n) {
+  hipError_t e = hipSuccess;
+  const bool lift_kernel = p->d.n_f64 != 0;
+  for (int i = 0; i < n && e == hipSuccess; ++i) {
+    if (!lift_kernel && i == 1) {
+      t[i] = 0;
+      continue;
+    }
+    e = hipEventElapsedTime(&t[i], p->ev[!lift_kernel && i == 2 ? 1 : i], p->ev[i + 1]);
+  }
+  return e;
 }
 bool ring_word_ok(uint64_t v) {
   constexpr uint64_t modulus = 1ull << 59, bound = 1ull << 20;
@@ -863,6 +894,12 @@ int praghip_token_plan_create(int device, const uint64_t* q, size_t primes, uint
   p->timing.upload_ms = ms;
   p->timing.device_bytes = p->buf.total_bytes();
   p->timing.sensitive_bytes = p->buf.sensitive_bytes();
+  p->phases.initial_input_upload_ms = ms;
+  p->phases.input_bytes = in_words * 8;
+  p->phases.ring_weight_bytes = blocks * width * 8;
+  p->phases.ntt_weight_bytes = blocks * primes * n * 8;
+  p->phases.output_bytes = words * 8;
+  p->phases.device_bytes = p->timing.device_bytes;
   *plan = p.release();
   return PRAGHIP_OK;
 }
@@ -900,26 +937,32 @@ int praghip_token_evaluate(praghip_token_plan* p, const uint64_t* ring, size_t w
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
   hipStream_t s = p->stream;
+  // events: 0 start, 1 uploaded, 2 lifted, 3 transformed, 4 summed (= 5,
+  // nothing to finish), 6 downloaded (resident.cu:152-166)
   if (e == hipSuccess) e = hipEventRecord(p->ev[0], s);
   if (e == hipSuccess) e = hipMemcpyAsync(p->ring, ring, words * 8, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipEventRecord(p->ev[1], s);
-  if (e == hipSuccess) e = token_product(p, p->ring, false, s);
-  if (e == hipSuccess) e = hipEventRecord(p->ev[2], s);
+  if (e == hipSuccess) e = token_product(p, p->ring, false, s, p->ev + 2);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[5], s);
   if (e == hipSuccess) e = hipMemcpyAsync(output, p->output, p->words * 8, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipEventRecord(p->ev[3], s);
-  if (e == hipSuccess) e = hipEventSynchronize(p->ev[3]);
-  float t01 = 0, t12 = 0, t23 = 0;
-  if (e == hipSuccess) e = hipEventElapsedTime(&t01, p->ev[0], p->ev[1]);
-  if (e == hipSuccess) e = hipEventElapsedTime(&t12, p->ev[1], p->ev[2]);
-  if (e == hipSuccess) e = hipEventElapsedTime(&t23, p->ev[2], p->ev[3]);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[6], s);
+  if (e == hipSuccess) e = hipEventSynchronize(p->ev[6]);
+  float t[6] = {};
+  if (e == hipSuccess) e = token_phase_times(p, t, 6);
   if (e != hipSuccess) {
     volatile uint64_t* o = output;
     for (size_t i = 0; i < p->words; ++i) o[i] = 0;
     return token_failure(p, e, "evaluate");
   }
-  p->timing.upload_ms = t01;
-  p->timing.kernel_ms = t12;
-  p->timing.download_ms = t23;
+  p->timing.upload_ms = t[0];
+  p->timing.kernel_ms = double(t[1]) + t[2] + t[3] + t[4];
+  p->timing.download_ms = t[5];
+  p->phases.weight_upload_ms = t[0];
+  p->phases.lift_ms = t[1];
+  p->phases.ntt_ms = t[2];
+  p->phases.dyadic_ms = double(t[3]) + t[4];
+  p->phases.finish_ms = 0;
+  p->phases.download_ms = t[5];
   return PRAGHIP_OK;
 }
 
@@ -928,21 +971,28 @@ static int token_finished_host(praghip_token_plan* p, const uint64_t* ring, size
   DeviceScope scope(p->device);
   hipError_t e = scope.status();
   hipStream_t s = p->stream;
+  // events: 0 start, 1 uploaded, 2 lifted, 3 transformed, 4 summed, 5
+  // finished (resident.cu:167-184)
   if (e == hipSuccess) e = hipEventRecord(p->ev[0], s);
   if (e == hipSuccess) e = hipMemcpyAsync(p->ring, ring, words * 8, hipMemcpyHostToDevice, s);
   if (e == hipSuccess && residues)
     e = hipMemcpyAsync(p->scaled, residues, p->slots * p->P * 8, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipEventRecord(p->ev[1], s);
-  if (e == hipSuccess) e = token_finished(p, p->ring, residues ? p->scaled : nullptr, p->finished, s);
-  if (e == hipSuccess) e = hipEventRecord(p->ev[2], s);
-  if (e == hipSuccess) e = hipEventSynchronize(p->ev[2]);
-  float t01 = 0, t12 = 0;
-  if (e == hipSuccess) e = hipEventElapsedTime(&t01, p->ev[0], p->ev[1]);
-  if (e == hipSuccess) e = hipEventElapsedTime(&t12, p->ev[1], p->ev[2]);
+  if (e == hipSuccess) e = token_finished(p, p->ring, residues ? p->scaled : nullptr, p->finished, s, p->ev + 2);
+  if (e == hipSuccess) e = hipEventRecord(p->ev[5], s);
+  if (e == hipSuccess) e = hipEventSynchronize(p->ev[5]);
+  float t[5] = {};
+  if (e == hipSuccess) e = token_phase_times(p, t, 5);
   if (e != hipSuccess) return token_failure(p, e, "evaluate_finished");
-  p->timing.upload_ms = t01;
-  p->timing.kernel_ms = t12;
+  p->timing.upload_ms = t[0];
+  p->timing.kernel_ms = double(t[1]) + t[2] + t[3] + t[4];
   p->timing.download_ms = 0;
+  p->phases.weight_upload_ms = t[0];
+  p->phases.lift_ms = t[1];
+  p->phases.ntt_ms = t[2];
+  p->phases.dyadic_ms = t[3];
+  p->phases.finish_ms = t[4];
+  p->phases.download_ms = 0;
   *view = p->finished;
   return PRAGHIP_OK;
 }
@@ -1117,6 +1167,12 @@ int praghip_token_download(praghip_token_plan* p, const uint64_t* view, uint64_t
 // download waiting on the view's ready event (resident.cu:187-189).
 int praghip_token_download_ready(praghip_token_plan* p, const uint64_t* view, void* ready, uint64_t* output) {
   return token_download(p, view, ready, true, output);
+}
+
+int praghip_token_phase_timing(const praghip_token_plan* p, praghip_token_phases* out) {
+  if (!p || !out) return fail(PRAGHIP_E_ARGUMENT, "E_NULL");
+  *out = p->phases;
+  return PRAGHIP_OK;
 }
 
 int praghip_token_timing(const praghip_token_plan* p, praghip_timing* out) {

@@ -32,6 +32,21 @@ class Timing(ctypes.Structure):
                 ("device_bytes", ctypes.c_uint64), ("sensitive_bytes", ctypes.c_uint64)]
 
 
+class SwitchPhases(ctypes.Structure):
+    """Switch::Timing (switch.hpp:10): praghip_switch_phases."""
+    _fields_ = [(n, ctypes.c_double) for n in ("setup_upload_ms", "upload_ms", "rns_ntt_ms", "product_ms",
+                                               "inverse_ms", "moddown_ms", "download_ms")] + \
+               [("device_bytes", ctypes.c_uint64), ("sensitive_bytes", ctypes.c_uint64)]
+
+
+class TokenPhases(ctypes.Structure):
+    """TokenWeights::Timing (resident.hpp:11-12): praghip_token_phases."""
+    _fields_ = [(n, ctypes.c_double) for n in ("initial_input_upload_ms", "weight_upload_ms", "lift_ms", "ntt_ms",
+                                               "dyadic_ms", "download_ms", "finish_ms")] + \
+               [(n, ctypes.c_uint64) for n in ("input_bytes", "ring_weight_bytes", "ntt_weight_bytes",
+                                                "output_bytes", "device_bytes")]
+
+
 vp, sz, u32, u64, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
 
 
@@ -74,12 +89,13 @@ SIGNATURES = {
     "praghip_ntt_timing": (i32, [vp, ctypes.POINTER(Timing)]),
     "praghip_ntt_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_ntt_destroy": (None, [vp]),
-    "praghip_switch_plan_create": (i32, [i32, vp, sz, u32, sz, vp, u32, sz, pp]),
+    "praghip_switch_plan_create": (i32, [i32, vp, sz, u32, sz, vp, vp, vp, vp, vp, u32, sz, pp]),
     "praghip_switch_apply": (i32, [vp, vp, vp]),
     "praghip_switch_evaluate": (i32, [vp, vp, vp]),
     "praghip_keyswitch": (i32, [vp, vp, vp, sz, vp, sz, u32, vp]),
     "praghip_switch_sync": (i32, [vp]),
     "praghip_switch_timing": (i32, [vp, ctypes.POINTER(Timing)]),
+    "praghip_switch_phase_timing": (i32, [vp, ctypes.POINTER(SwitchPhases)]),
     "praghip_switch_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_switch_destroy": (None, [vp]),
     "praghip_share_gemm": (i32, [i32, vp, vp, i32, vp, vp, sz, sz, sz, i32, vp]),
@@ -132,6 +148,7 @@ SIGNATURES = {
     "praghip_token_stack_store_ready": (i32, [vp, sz, ctypes.c_uint, vp, vp]),
     "praghip_token_download_ready": (i32, [vp, vp, vp, vp]),
     "praghip_token_timing": (i32, [vp, ctypes.POINTER(Timing)]),
+    "praghip_token_phase_timing": (i32, [vp, ctypes.POINTER(TokenPhases)]),
     "praghip_token_close": (i32, [vp, ctypes.POINTER(Cleanup)]),
     "praghip_token_destroy": (None, [vp]),
     "praghip_pack_plan_create": (i32, [i32, vp, sz, u32, sz, sz, vp, sz, pp]),

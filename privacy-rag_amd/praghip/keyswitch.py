@@ -5,7 +5,7 @@ import ctypes
 
 import numpy as np
 
-from ._lib import Cleanup, Timing, check, lib, shape_error
+from ._lib import Cleanup, SwitchPhases, Timing, check, lib, shape_error
 from ._util import dev_ptr, host_ptr, host_u64, stream_handle, u64_dtypes
 
 
@@ -15,9 +15,16 @@ class Switch:
     ``key``: host [dnum][2][L+1][N] NTT-form switching key for ``element`` (or
     None when keys are passed per call).  dnum = L is the reference's one prime
     per digit; dnum < L uses fast base conversion.
+
+    ``tables``: optional dict of the SEAL arrays ``Switch::initialize(q, f, r,
+    ni, invp, keys)`` takes (switch.hpp:24, keyswitch/seal_adapter.cpp:24-41):
+    ``fwd`` / ``inv`` [L+1][N][2], ``invn`` [L+1][2], ``invp`` [L][2]
+    (inv_q_last_mod_q).  Each given array is checked against the one derived
+    from q (E_NTT_CONTEXT on a mismatch).
     """
 
-    def __init__(self, q, log_n: int, dnum: int, key=None, element: int = 1, max_batch: int = 1, device: int = 0):
+    def __init__(self, q, log_n: int, dnum: int, key=None, element: int = 1, max_batch: int = 1, device: int = 0,
+                 tables=None):
         self.q = [int(x) for x in q]
         self.L = len(self.q) - 1
         self.log_n = log_n
@@ -27,8 +34,23 @@ class Switch:
         k = None if key is None else host_u64(key)
         if k is not None and k.size != dnum * 2 * (self.L + 1) << log_n:
             raise shape_error("E_SWITCH_KEY_SHAPE")
+        tables = tables or {}
+        K, n = self.L + 1, 1 << log_n
+        sizes = {"fwd": K * n * 2, "inv": K * n * 2, "invn": K * 2, "invp": self.L * 2}
+        unknown = set(tables) - set(sizes)
+        if unknown:
+            raise ValueError(f"unknown table names {sorted(unknown)}")
+        arrs = {}
+        for name, size in sizes.items():
+            t = tables.get(name)
+            if t is None:
+                continue
+            arrs[name] = host_u64(t)
+            if arrs[name].size != size:
+                raise shape_error("E_NTT_CONTEXT")
+        tp = [host_ptr(arrs[nm]) if nm in arrs else None for nm in ("fwd", "inv", "invn", "invp")]
         h = ctypes.c_void_p()
-        check(lib().praghip_switch_plan_create(device, host_ptr(qa), self.L, log_n, dnum,
+        check(lib().praghip_switch_plan_create(device, host_ptr(qa), self.L, log_n, dnum, *tp,
                                                None if k is None else host_ptr(k), element, max_batch,
                                                ctypes.byref(h)))
         self._h = h
@@ -78,6 +100,12 @@ class Switch:
     def timing(self) -> Timing:
         t = Timing()
         check(lib().praghip_switch_timing(self._h, ctypes.byref(t)))
+        return t
+
+    def phase_timing(self) -> SwitchPhases:
+        """Switch::timing (switch.hpp:10): phases of the last apply / evaluate."""
+        t = SwitchPhases()
+        check(lib().praghip_switch_phase_timing(self._h, ctypes.byref(t)))
         return t
 
     def close(self) -> Cleanup:

@@ -9,7 +9,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import Cleanup, Timing, check, lib, shape_error
+from ._lib import Cleanup, Timing, TokenPhases, check, lib, shape_error
 from ._util import dev_ptr, host_u64, stream_handle, u64_dtypes
 
 
@@ -140,6 +140,12 @@ class TokenWeights:
     def timing(self) -> Timing:
         t = Timing()
         check(lib().praghip_token_timing(self._h, ctypes.byref(t)))
+        return t
+
+    def phase_timing(self) -> TokenPhases:
+        """TokenWeights::timing (resident.hpp:11-12): phases of the last host-buffer evaluation."""
+        t = TokenPhases()
+        check(lib().praghip_token_phase_timing(self._h, ctypes.byref(t)))
         return t
 
     def close(self) -> Cleanup:

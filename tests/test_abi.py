@@ -82,6 +82,40 @@ def test_plan_validation_before_device():
     assert e.value.code == _lib.E_ARGUMENT
 
 
+def seal_switch_tables(q, log_n):
+    """The arrays the reference's Switch::initialize(q, f, r, ni, invp, keys)
+    receives (keyswitch/seal_adapter.cpp:24-41): SEAL's root-power tables from
+    the oracle, and inv_q_last_mod_q computed here from the definition
+    (q[L]^-1 mod q_i with its Shoup quotient floor(w 2^64 / q_i))."""
+    t = oracle.Tables(q, log_n)
+    invp = []
+    for qi in q[:-1]:
+        w = pow(q[-1] % qi, qi - 2, qi)
+        assert w * q[-1] % qi == 1
+        invp += [w, (w << 64) // qi]
+    return {"fwd": t.fwd, "inv": t.inv, "invn": t.invn, "invp": np.array(invp, dtype=np.uint64)}
+
+
+def test_switch_takes_and_checks_seal_tables():
+    """Switch::initialize's tables: the right ones pass validation (the call
+    then stops only at the device check here), and one corrupted operand or
+    quotient in any of them is E_NTT_CONTEXT before any device call."""
+    q, log_n = cf.LOCKED_PRIMES, 10
+    good = seal_switch_tables(q, log_n)
+    if praghip.device_count() == 0:
+        with pytest.raises(praghip.PraghipError) as e:
+            praghip.Switch(q, log_n, dnum=6, tables=good)
+        assert e.value.code == _lib.E_DEVICE
+    for name, idx in (("fwd", (3, 77, 1)), ("inv", (6, 5, 0)), ("invn", (2, 1)), ("invp", (9,))):
+        bad = {k: v.copy() for k, v in good.items()}
+        bad[name][idx] ^= 1
+        with pytest.raises(praghip.PraghipError) as e:
+            praghip.Switch(q, log_n, dnum=6, tables=bad)
+        assert e.value.code == _lib.E_CONTEXT and "E_NTT_CONTEXT" in e.value.text, name
+    with pytest.raises(ValueError):
+        praghip.Switch(q, log_n, dnum=6, tables={"forward": good["fwd"]})
+
+
 def test_no_device_here_is_reported():
     if praghip.device_count() > 0:
         pytest.skip("a GPU is present")

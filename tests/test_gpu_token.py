@@ -84,6 +84,12 @@ def test_token_reference_size(gpu, slots):
     batch = tw.evaluate_local_finished(ring)
     for s in range(slots):
         np.testing.assert_array_equal(tw.download(tw.slot_view(batch, s)), want_local[s], err_msg=f"local slot {s}")
+    # TokenWeights::Timing (resident.hpp:11-12) of that call: the lift is in
+    # the transform's loads on the locked primes, the phases sum to the kernel time
+    ph, t = tw.phase_timing(), tw.timing()
+    assert ph.ntt_ms > 0 and ph.dyadic_ms > 0 and ph.finish_ms > 0 and ph.lift_ms == 0
+    assert abs(ph.lift_ms + ph.ntt_ms + ph.dyadic_ms + ph.finish_ms - t.kernel_ms) <= 0.05 * t.kernel_ms
+    assert ph.initial_input_upload_ms > 0 and ph.ntt_weight_bytes == blocks * 6 * n * 8
     # device entry point, explicit residues and bound shares
     import torch
     out = to_dev(np.zeros((slots, 2, 6, n), dtype=np.uint64))
@@ -117,6 +123,10 @@ def test_token_shapes(gpu, log_n, P, blocks, slots, width):
     batch = tw.evaluate_finished(ring, local)
     for s in range(slots):
         np.testing.assert_array_equal(tw.download(tw.slot_view(batch, s)), want[s])
+    # 50-bit primes: the lift is a kernel of its own, timed apart
+    ph, t = tw.phase_timing(), tw.timing()
+    assert ph.lift_ms > 0 and ph.ntt_ms > 0 and ph.dyadic_ms > 0 and ph.finish_ms > 0
+    assert abs(ph.lift_ms + ph.ntt_ms + ph.dyadic_ms + ph.finish_ms - t.kernel_ms) <= 0.05 * t.kernel_ms
     tw.close()
 
 
