@@ -56,6 +56,11 @@ struct KsRows {
   unsigned b0, cts;  // chunk: ciphertexts b0 .. b0 + cts - 1
 };
 
+template <class A>
+struct TypeTag {
+  using type = A;
+};
+
 __device__ __forceinline__ uint64_t bits_of(double x) { return (uint64_t)__double_as_longlong(x); }
 __device__ __forceinline__ double double_of(uint64_t x) { return __longlong_as_double((long long)x); }
 
@@ -194,13 +199,13 @@ __device__ __forceinline__ void digit_factors(uint64_t (&y)[D][kE], const KsRows
   }
 }
 
-// Targets per column-forward thread: the digit's column is read and its
-// factors y computed once for G targets (all six float-path data primes at
-// L = 6: c1 is then read once per digit, instead of once per target group on
-// different XCDs).  On the integer path one-prime digits take every key
-// prime (their stores then overlap the next target's stages: 123 -> 103 us
-// at dnum = 6, batch 64); larger digits one target, since their factors
-// would not fit the registers beside a second target's values.
+// Targets per integer-path column-forward thread (cols_fwd_body): the
+// digit's column is read and its factors y computed once for G targets.
+// One-prime digits take every key prime (their stores then overlap the next
+// target's stages: 123 -> 103 us at dnum = 6, batch 64); larger digits one
+// target, since their factors would not fit the registers beside a second
+// target's values.  (The float-path data primes take every target of a digit
+// in cols_fwd_float_body.)
 template <class A, int D>
 constexpr unsigned kColTargets() {
   return std::is_same<typename A::T, double>::value ? 6u : (D == 1 ? 7u : 1u);
@@ -283,16 +288,83 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kColFw
   cols_fwd_body<D, A, G>(f, t_lo, t_n, blockIdx.x);
 }
 
-// Both policies in one launch when both are present: the first nu blocks
-// take the integer-path primes t_u64 .. t_u64 + n_u64 - 1 (policy AU: ArU64L
-// when every key prime is below 2^60, else ArU64), the rest the float-path
-// data primes, so the special prime's 64-bit work overlaps the float targets
-// instead of running after them.
+// The float-path data primes of one digit column in one thread: thread
+// (ciphertext, digit j, column c) reads the digit's D residues at its column
+// once, transforms them as the digit's own targets, turns them into the
+// factors [x (Q_j/q_i)^-1]_{q_i} in place and base-converts them to every
+// other data prime.  `w` names the (ciphertext, digit, 256 columns) the
+// workgroup takes, as in cols_fwd_body with one target group.
+template <int D>
+__device__ __forceinline__ void cols_fwd_float_body(const KsRows& f, unsigned w_blk) {
+  const KsConst& kc = *f.kc;
+  const unsigned dnum = unsigned(kc.dnum), K = unsigned(kc.K), L = unsigned(kc.L);
+  const unsigned gid = w_blk * blockDim.x + threadIdx.x;
+  if (gid >= f.cts * dnum * kCols) return;
+  const unsigned w = __builtin_amdgcn_readfirstlane(gid >> kRowLog);  // kCols is a multiple of the wave size
+  const unsigned c = gid & (kCols - 1), j = w % dnum, bl = w / dnum, b = f.b0 + bl;
+  const int lo = kc.dig_lo[j];
+  const uint64_t* c1 = f.in + ((size_t(b) * 2 + 1) * L << kLog);
+  uint64_t* eb = f.e + (size_t(bl) * dnum + j) * K * kN + c;
+  const auto store = [&](int t, const double (&v)[kE]) {
+    uint64_t* et = eb + (size_t(t) << kLog);
+#pragma unroll
+    for (int k = 0; k < kE; ++k) et[unsigned(k) << kRowLog] = bits_of(v[k]);
+  };
+  uint64_t y[D][kE];
+#pragma unroll
+  for (int d = 0; d < D; ++d) gather_column(y[d], c1 + (size_t(lo + d) << kLog), c, f.ginv, kc.q[lo + d]);
+  // the digit's own primes: their residues as they are
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const ArF64Lean ar(f.primes[lo + d]);
+    double v[kE];
+#pragma unroll
+    for (int k = 0; k < kE; ++k) v[k] = ArF64::from_u64(y[d][k]);
+    top_fwd<ArF64Lean, true>(v, f.tw_fwd_f + (size_t(lo + d) << kLog), ar);
+    store(lo + d, v);
+  }
+  if constexpr (D > 1) {  // factors in place (exact FP64 products, canonical)
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const NttPrime pi = f.primes[lo + d];
+      const double iw = double(kc.inv_hat[lo + d].w), iwq = iw * pi.qinv;
+#pragma unroll
+      for (int k = 0; k < kE; ++k)
+        y[d][k] = (uint64_t)canon_f64(mul_f64(ArF64::from_u64(y[d][k]), iw, iwq, pi.qd), pi.qd);
+    }
+  }
+  for (int t = 0; t < int(L); ++t) {  // the other data primes
+    if (t >= lo && t < lo + D) continue;
+    const NttPrime pt = f.primes[t];
+    const ArF64Lean ar(pt);
+    double v[kE];
+    if constexpr (D == 1) {
+#pragma unroll
+      for (int k = 0; k < kE; ++k) v[k] = ArF64::from_u64(reduce_to(y[0][k], kc, t, f.narrow));
+    } else {
+      cols_target_f64<D>(v, y, kc, lo, t, pt);
+    }
+    top_fwd<ArF64Lean, true>(v, f.tw_fwd_f + (size_t(t) << kLog), ar);
+    store(t, v);
+  }
+}
+
+// Float-path data primes with an integer-path special prime: a workgroup
+// takes the float targets or the special prime of one (ciphertext, digit, 256
+// columns); workgroups go to the XCDs round robin, so in every run of 16 the
+// first eight take the float targets of eight column groups and the next
+// eight the special prime of the same eight, on the same XCDs and dispatched
+// together - the special prime's read of the digit's columns finds them in
+// that XCD's L2.  Each digit column is read from memory once.
 template <int D, class AU>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1 ? 3 : 2)))
-    ks_cols_fwd_both(KsRows f, unsigned t_u64, unsigned n_u64, unsigned nu) {
-  if (blockIdx.x < nu) cols_fwd_body<D, AU, kColTargets<AU, D>()>(f, t_u64, n_u64, blockIdx.x);
-  else cols_fwd_body<D, ArF64Lean, kColTargets<ArF64Lean, D>()>(f, 0u, t_u64, blockIdx.x - nu);
+    ks_cols_fwd_pair(KsRows f, unsigned works) {
+  const unsigned r = blockIdx.x & 15u, w = (blockIdx.x >> 4) * 8u + (r & 7u);
+  if (w >= works) return;
+  if (r < 8)
+    cols_fwd_float_body<D>(f, w);
+  else
+    cols_fwd_body<D, AU, 1>(f, unsigned(f.kc->L), 1u, w);
 }
 
 // ------------------------------------------------------------------ phase B
@@ -530,8 +602,10 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
     }
   }
   uint64_t* pb = f.prod + ((size_t(b) * 2 * K + t) << kLog) + (row << kRowLog);
-  // the lazy path's inverse passes with the compiler's Shoup product (ArU64LC)
-  const std::conditional_t<kMont, ArU64LC, A> ari(pr);
+  // the integer paths' inverse passes with the compiler's Shoup product
+  // (ArU64LC, ArU64C)
+  using AI = std::conditional_t<kMont, ArU64LC, std::conditional_t<std::is_same<A, ArU64>::value, ArU64C, A>>;
+  const AI ari(pr);
   row_passes_e<true, 0>(a0, lds, t2, row, ti, ari, pr);
 #pragma unroll
   for (int k = 0; k < E; ++k) pb[inv_out_index<kRowLog, kRowLE>(t2, k)] = store_form<A>(a0[k]);
@@ -714,19 +788,23 @@ static int uniform_digit(const KsConst& kc) {
 template <int D, class AU>
 static void launch_cols_fwd(const KsRows& f, unsigned dnum, unsigned t_u64, unsigned K, hipStream_t s) {
   const auto grid = [&](unsigned t_n, unsigned g) { return dim3((f.cts * dnum * ((t_n + g - 1) / g) * kCols + 255) / 256); };
-  constexpr unsigned GU = kColTargets<ArU64, D>(), GF = kColTargets<ArF64Lean, D>();
+  constexpr unsigned GU = kColTargets<ArU64, D>();
   if (!t_u64) {  // every prime on the integer path
     hipLaunchKernelGGL((ks_cols_fwd_kernel<D, AU, GU>), grid(K, GU), dim3(256), 0, s, f, 0u, K);
     return;
   }
-  const unsigned nu = grid(K - t_u64, GU).x, nf = grid(t_u64, GF).x;
-  hipLaunchKernelGGL((ks_cols_fwd_both<D, AU>), dim3(nu + nf), dim3(256), 0, s, f, t_u64, K - t_u64, nu);
+  // float data primes, integer special prime (t_u64 = L, K = L + 1)
+  const unsigned works = f.cts * dnum * kCols / 256;
+  hipLaunchKernelGGL((ks_cols_fwd_pair<D, AU>), dim3((works + 7) / 8 * 16), dim3(256), 0, s, f, works);
 }
 
 // One chunk of ciphertexts through the four launches, the integer-path
 // primes on policy AU.
 template <class AU>
-static void launch_chunk(const KsRows& f, const KsConst& kc, int dig, hipStream_t s) {
+static void launch_chunk(const KsRows& f, const KsConst& kc, int dig, hipStream_t s, hipEvent_t* ev) {
+  const auto mark = [&](int i) {
+    if (ev) (void)hipEventRecord(ev[i], s);
+  };
   const unsigned K = unsigned(kc.K), L = unsigned(kc.L), dnum = unsigned(kc.dnum), rows = kN >> kRowLog;
   // the integer-path primes t_u64 .. K - 1 (the special prime, or every
   // prime when a data prime has 50 bits or more), the float-path data
@@ -737,14 +815,18 @@ static void launch_chunk(const KsRows& f, const KsConst& kc, int dig, hipStream_
     case 2: launch_cols_fwd<2, AU>(f, dnum, t_u64, K, s); break;
     default: launch_cols_fwd<3, AU>(f, dnum, t_u64, K, s); break;
   }
+  mark(0);
   const unsigned items = f.cts * K * rows;
   hipLaunchKernelGGL(ks_rows2_kernel<AU>, dim3(items), dim3(kRow2Threads), 0, s, f, t_u64);
+  mark(1);
   hipLaunchKernelGGL(ks_cols_special_kernel<AU>, dim3((f.cts * 2 * kCols + 255) / 256), dim3(256), 0, s, f);
+  mark(2);
   const dim3 c_grid((f.cts * 2 * L * kCols + 255) / 256);
   if (f.data_f64)
     hipLaunchKernelGGL(ks_cols_inv_kernel<ArF64>, c_grid, dim3(256), 0, s, f);
   else
     hipLaunchKernelGGL(ks_cols_inv_kernel<AU>, c_grid, dim3(256), 0, s, f);
+  mark(3);
 }
 
 bool keyswitch_rows_supported(const KsConst& kc) {
@@ -788,10 +870,12 @@ hipError_t launch_keyswitch_rows(const KsArgs& a, const KsConst* kc_dev, const K
     f.cts = unsigned(std::min<size_t>(a.inter_cts, a.batch - b0));
     // every key prime below 2^60: the lazy integer path with Montgomery key
     // products (KsConst::lazy); else Harvey's bounds and Shoup key products
+    // phase events only when the whole batch is one chunk
+    hipEvent_t* ev = a.batch <= a.inter_cts ? a.phase_events : nullptr;
     if (kc.lazy)
-      launch_chunk<ArU64L>(f, kc, dig, s);
+      launch_chunk<ArU64L>(f, kc, dig, s, ev);
     else
-      launch_chunk<ArU64>(f, kc, dig, s);
+      launch_chunk<ArU64>(f, kc, dig, s, ev);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -171,12 +171,27 @@ struct ArU64L : ArU64 {
   }
 };
 
-// ArU64L whose inverse butterfly takes the compiler's Shoup product: the
-// keyswitch rows kernel's inverse passes.  With the carry-out product both in
-// those passes and in the kernel's Montgomery key products, every twiddle
-// product of the rows' inverse passes came out wrong on the GPU (each of the
-// two alone was exact, and no hazard or register conflict showed in the
-// compiled code); this split keeps both kernels' tests exact.
+// ArU64 and ArU64L whose inverse butterfly takes the compiler's Shoup
+// product: the keyswitch rows kernel's inverse passes.  With the carry-out
+// product there, every twiddle product of those passes came out wrong on the
+// GPU - with the lazy form and Montgomery key products (each of the two alone
+// was exact), and with the per-stage form and Shoup key products (a 62-bit
+// special prime) - while the same product is exact in the rows' forward
+// passes and in every other transform.  The compiled code shows no wait-state
+// shortfall, no write of the carry between its producer and its reader and
+// no spill; the cause is not known, so these passes keep the compiler's
+// product.
+struct ArU64C : ArU64 {
+  __device__ explicit ArU64C(const NttPrime& p) : ArU64(p) {}
+  template <bool = false>
+  __device__ __forceinline__ void inv(T& x, T& y, TW w) const {
+    T s = x + y;
+    s = s >= q2 ? s - q2 : s;
+    const T d = x - y + q2;
+    x = s;
+    y = mul_shoup_lazy(d, w.x, w.y, q);
+  }
+};
 struct ArU64LC : ArU64L {
   __device__ explicit ArU64LC(const NttPrime& p) : ArU64L(p) {}
   template <bool = false>

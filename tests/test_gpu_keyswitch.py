@@ -220,3 +220,40 @@ def test_keyswitch_data_prime_below_2_32(gpu):
     tin, tout = to_dev(ct), to_dev(np.zeros_like(ct))
     sw.keyswitch(tin, tout, keys=to_dev(keys), key_stride=sw.key_words, galois=3)
     np.testing.assert_array_equal(from_dev(tout), want)
+
+
+def test_keyswitch_with_seal_tables_and_phase_timing(gpu):
+    """Switch::initialize(q, f, r, ni, invp, keys) with the SEAL tables passed
+    in (switch.hpp:24): the plan accepts them and switches exactly as the
+    oracle; the per-phase times of Switch::Timing (switch.hpp:10) sum to the
+    kernel time."""
+    from test_abi import seal_switch_tables
+    q, n, L, dnum = cf.LOCKED_PRIMES, 16384, 6, 6
+    print("[ks] seal tables dnum=6", flush=True)
+    ct = oracle.fill_residues(2 * L, n, q[:L], 0x5052414700000903).reshape(1, 2, L, n)
+    key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 0x5052414700010903).reshape(dnum, 2, L + 1, n)
+    sw = praghip.Switch(q, 14, dnum, key=key, element=3, tables=seal_switch_tables(q, 14))
+    np.testing.assert_array_equal(sw.apply(ct[0]), oracle.keyswitch(ct, key, q, dnum, 14, 3)[0])
+    ph, t = sw.phase_timing(), sw.timing()
+    parts = [ph.rns_ntt_ms, ph.product_ms, ph.inverse_ms, ph.moddown_ms]
+    assert all(x > 0 for x in parts) and ph.setup_upload_ms > 0 and ph.upload_ms > 0 and ph.download_ms > 0
+    assert abs(sum(parts) - t.kernel_ms) <= 0.05 * t.kernel_ms
+    assert ph.device_bytes == t.device_bytes and ph.sensitive_bytes == t.sensitive_bytes
+
+
+@pytest.mark.parametrize("bits,dnum", [(61, 1), (62, 2), (62, 3)])
+def test_keyswitch_wide_special_prime_three_phase(gpu, bits, dnum):
+    """A special prime of 61 or 62 bits (the API takes primes up to 2^62): the
+    three-phase path at N = 16384 then runs the per-stage Harvey transforms
+    and Shoup key products (no key prime below 2^60 for the lazy form)."""
+    q = cf.primes_below(50, 16384, 6) + cf.primes_below(bits, 16384, 1)
+    n, L, batch = 16384, 6, 2
+    print(f"[ks] special prime {bits} bits dnum={dnum}", flush=True)
+    ct = oracle.fill_residues(batch * 2 * L, n, q[:L], 0x5052414700000a03 + bits).reshape(batch, 2, L, n)
+    keys = oracle.fill_residues(batch * dnum * 2 * (L + 1), n, q, 0x5052414700010a03 + dnum).reshape(
+        batch, dnum, 2, L + 1, n)
+    want = oracle.keyswitch(ct, keys, q, dnum, 14, 3, per_ct_keys=True)
+    sw = praghip.Switch(q, 14, dnum, max_batch=batch)
+    tin, tout, tk = to_dev(ct), to_dev(np.zeros_like(ct)), to_dev(keys)
+    sw.keyswitch(tin, tout, keys=tk, key_stride=sw.key_words, galois=3)
+    np.testing.assert_array_equal(from_dev(tout), want)
