@@ -33,20 +33,69 @@ N = 16384
 LOG_N = 14
 
 
-def measured_traffic(workload: str, launches_per_step: int):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (profiles/hbm_traffic.json), scaled by the copy calibration; None
-    when no summary is committed for the workload."""
-    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+# Committed rocprofv3 summaries behind each leg's `traffic`: the summary under
+# profiles/, a pattern for the kernels of one timed step, and the launches the
+# step's bytes are divided over (None: the average over the matching kernels'
+# dispatches, for a leg whose step launches the same kernel on many shapes).
+TRAFFIC_SOURCES = {
+    "ntt": ("ntt_n16384_3072limbs.md", r"ntt_kernel<14,", 2),
+    "keyswitch": ("keyswitch_n16384_L6_dnum3_batch64.md", r"ks_", 1),
+    "keyswitch_reference": ("keyswitch_n16384_locked_dnum6_batch64.md", r"ks_", 1),
+    "gemm": ("share_gemm_512x1024x3072_i8.md", r"share_gemm_dma_kernel", 1),
+    "gemm_f12": ("share_gemm_512x1024x3072_f12.md", r"share_gemm_dma_kernel|gemm_clear_kernel", 1),
+    "qwen3": ("qwen3_0.6b_local_gemms_28_layers.md", r"share_gemm_dma_kernel", None),
+}
+
+
+def profile_counters(name: str):
+    """{kernel: {counter: (average per dispatch, dispatches)}} from the
+    'Counters (average per dispatch)' table of a committed summary."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
+    out = {}
     with open(path) as f:
-        t = json.load(f)
-    if workload not in t:
+        for line in f:
+            cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+            if len(cells) == 4 and cells[1].isupper() and cells[3].isdigit():
+                try:
+                    out.setdefault(cells[0], {})[cells[1]] = (float(cells[2]), int(cells[3]))
+                except ValueError:
+                    continue
+    return out
+
+
+def copy_calibration():
+    """FETCH_SIZE and WRITE_SIZE scale factors from the 384 MiB device copy
+    (profiles/copy_384MiB_calibration.md): true KiB / counted KiB."""
+    c = profile_counters("copy_384MiB_calibration.md")
+    if not c or "__amd_rocclr_copyBuffer" not in c:
         return None
-    fs, ws = t["calibration"]["fetch_scale"], t["calibration"]["write_scale"]
-    total = sum(fs * k["FETCH_SIZE_KiB"] + ws * k["WRITE_SIZE_KiB"] for k in t[workload]["kernels"].values())
-    return int(total * 1024 / launches_per_step)
+    k = c["__amd_rocclr_copyBuffer"]
+    true_kib = 3072 * N * 8 / 1024
+    return round(true_kib / k["FETCH_SIZE"][0], 2), round(true_kib / k["WRITE_SIZE"][0], 2)
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch (per step for multi-kernel legs) from the FETCH_SIZE
+    and WRITE_SIZE rows of the workload's committed rocprofv3 summary, scaled
+    by the copy calibration; None without a summary."""
+    src, cal = TRAFFIC_SOURCES.get(workload), copy_calibration()
+    if not src or not cal:
+        return None
+    name, pattern, launches = src
+    c = profile_counters(name)
+    if not c:
+        return None
+    import re
+    per = {k: (cal[0] * v["FETCH_SIZE"][0] + cal[1] * v["WRITE_SIZE"][0]) * 1024
+           for k, v in c.items() if re.match(pattern, k) and "FETCH_SIZE" in v and "WRITE_SIZE" in v}
+    if not per:
+        return None
+    if launches is None:  # average over the matching dispatches
+        d = {k: c[k]["FETCH_SIZE"][1] for k in per}
+        return int(sum(per[k] * d[k] for k in per) / sum(d.values()))
+    return int(sum(per.values()) / launches)
 
 
 def log(msg: str) -> None:
@@ -95,16 +144,19 @@ def bench_ntt(torch, praghip, steps, warmup):
         "limbs": limbs, "q": q, "ms_per_step": ms, "launch_ms": launch_ms,
         "ntt_per_s": 2 * limbs / (ms * 1e-3), "poly_ntt_per_s": 2 * limbs / 6 / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("ntt", 2),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("ntt"),
                      "kernel": "ntt_kernel<14> (forward and inverse launches)",
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
 
 
-def bench_keyswitch(torch, praghip, steps, warmup, reference=False):
+def bench_keyswitch(torch, praghip, steps, warmup, reference=False, galois=1):
     """64 keyswitches with their own keys at N=16384, L=6: dnum=3 over six
     ~50-bit data primes + a 60-bit special prime, or (reference=True) the
-    reference's own shape, dnum=6 over the seven locked 60-bit primes."""
+    reference's own shape, dnum=6 over the seven locked 60-bit primes.
+    galois: 1 is relinearization; an odd element (3: the rotation by one
+    slot's generator) gathers c1 through the automorphism inside the ModUp
+    reads and c0 inside the ModDown."""
     from praghip import params, synth
     q = list(params.LOCKED_PRIMES) if reference else params.primes_n16384_switch()
     L, dnum, batch = 6, (6 if reference else 3), 64
@@ -116,7 +168,7 @@ def bench_keyswitch(torch, praghip, steps, warmup, reference=False):
     synth.fill_residues(keys, q, LOG_N, 0x5052414700000103)
 
     def step():
-        sw.keyswitch(ct, out, keys=keys, key_stride=sw.key_words, galois=1)
+        sw.keyswitch(ct, out, keys=keys, key_stride=sw.key_words, galois=galois)
 
     ms = Timer(torch).run(step, steps, warmup)
     first = out.clone()
@@ -126,10 +178,10 @@ def bench_keyswitch(torch, praghip, steps, warmup, reference=False):
     bytes_per_ks = 8 * N * (2 * L + 2 * L + dnum * 2 * (L + 1))
     gbs = batch * bytes_per_ks / (ms * 1e-3) / 1e9
     return {
-        "batch": batch, "dnum": dnum, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
+        "batch": batch, "dnum": dnum, "galois": galois, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("keyswitch_reference" if reference else "keyswitch", 1),
+                     "traffic": None if galois != 1 else measured_traffic("keyswitch_reference" if reference else "keyswitch"),
                      "kernel": "whole keyswitch batch (all its launches); traffic is per batch",
                      "algorithmic_bytes_per_batch": batch * bytes_per_ks,
                      "algorithmic_bytes_per_keyswitch": bytes_per_ks},
@@ -163,7 +215,7 @@ def bench_gemm(torch, praghip, steps, warmup):
                       "kernel": "share_gemm_valu_kernel (v_dot4_i32_i8, same digit planes)",
                       "mfma_speedup": ms_valu / ms},
         "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm", 1),
+                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm"),
                      "kernel": "share_gemm_dma_kernel (i8 MFMA ops executed)"},
         "_tensors": (x, w, y),
     }
@@ -194,7 +246,7 @@ def bench_gemm_f12(torch, praghip, steps, warmup):
         "shape": [m, k, n], "weights": "int32 f12, |w| <= 2^20, pre-split into 3 int8 planes",
         "ms_per_step": ms, "tops": tops,
         "roofline": {"bound": "mfma", "achieved": round(mfma_tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm_f12", 1),
+                     "frac": round(mfma_tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("gemm_f12"),
                      "kernel": "share_gemm_dma_kernel, 3 weight planes (i8 MFMA ops executed)"},
         "_tensors": (x, w, y),
     }
@@ -211,7 +263,7 @@ def bench_qwen3(torch, praghip, steps, warmup):
             "layers_per_s": m.shape.layers / (ms * 1e-3), "tops": tops,
             "ops_per_forward": m.ops,
             "roofline": {"bound": "mfma", "achieved": round(8 * tops, 2), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
-                         "frac": round(8 * tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("qwen3", 1),
+                         "frac": round(8 * tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("qwen3"),
                          "kernel": "share_gemm_dma_kernel over the 112 products (i8 MFMA ops executed); "
                                    "traffic is the average per product"},
             "_model": m}
@@ -353,69 +405,98 @@ def bench_copy(torch, steps, warmup):
     return {"bytes_each_way": nbytes, "ms_per_step": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baselines(torch, res, budget_s: float):
-    """Oracle timings on bounded samples (rank 0, N=1 only)."""
+    """Oracle timings on bounded samples (rank 0, N=1 only).  Every leg runs
+    twice: on all host threads (OpenMP over limbs / ciphertexts / rows; its
+    output checked against the GPU's for the same inputs), and on one thread
+    over a smaller part of the same sample, as the reference's CPU path runs
+    (one limb at a time on one core, bfv.cpp:499-517; the scalar GEMM loop
+    bfv_matrix.inc:177-182)."""
     import numpy as np
 
     import oracle
     threads = len(os.sched_getaffinity(0))
+    model = cpu_model()
     out = {}
-    # NTT: sample of the 3072-limb batch, all host threads
+
+    def leg(name, rate, unit, sample, one_core_rate, one_core_sample):
+        out[name] = {"value": rate, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+                     "value_1core": one_core_rate, "sample_1core": one_core_sample, "cpu_model": model}
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        r = fn()
+        return r, time.perf_counter() - t0
+
+    # NTT: sample of the 3072-limb batch
     q = res["ntt"]["q"]
     tab = oracle.Tables(q, LOG_N)
     limbs = 384
     a = oracle.fill_residues(limbs, N, q, 0x5052414700000002)
-    t0 = time.perf_counter()
-    fa = oracle.ntt(a, tab, threads=threads)
-    oracle.ntt(fa, tab, inverse=True, threads=threads)
-    dt = time.perf_counter() - t0
+    _, dt = timed(lambda: oracle.ntt(oracle.ntt(a, tab, threads=threads), tab, inverse=True, threads=threads))
     reps = max(1, int(budget_s / 3 / max(dt, 1e-3)))
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        oracle.ntt(oracle.ntt(a, tab, threads=threads), tab, inverse=True, threads=threads)
-    dt = (time.perf_counter() - t0) / reps
-    out["ntt"] = {"value": 2 * limbs / dt, "unit": "limb-NTT/s", "cores": threads, "kind": "port",
-                  "sample": f"{limbs} limbs of the 3072-limb N=16384 batch, forward+inverse, x{reps}"}
-    # keyswitch: a few of the 64 ciphertexts with their keys
+    _, dt = timed(lambda: [oracle.ntt(oracle.ntt(a, tab, threads=threads), tab, inverse=True, threads=threads)
+                           for _ in range(reps)])
+    dt /= reps
+    a1 = a[:24]
+    back, dt1 = timed(lambda: oracle.ntt(oracle.ntt(a1, tab, threads=1), tab, inverse=True, threads=1))
+    assert np.array_equal(back, a1), "oracle NTT round trip"
+    leg("ntt", 2 * limbs / dt, "limb-NTT/s", f"{limbs} limbs of the 3072-limb N=16384 batch, forward+inverse, x{reps}",
+        2 * 24 / dt1, "24 limbs of the same batch, forward+inverse, one thread")
+    # keyswitch (dnum = 3): a few of the 64 ciphertexts with their keys
     ct_t, keys_t, out_t, q3 = res["keyswitch"]["_tensors"]
-    nb = 2 * threads if threads <= 8 else threads
-    nb = min(nb, 64)
+    nb = min(2 * threads if threads <= 8 else threads, 64)
     ct = ct_t[: nb * 2 * 6 * N].cpu().numpy().view(np.uint64).reshape(nb, 2, 6, N)
     kw = 3 * 2 * 7 * N
     keys = keys_t[: nb * kw].cpu().numpy().view(np.uint64).reshape(nb, 3, 2, 7, N)
-    tab3 = oracle.Tables(q3, LOG_N)
-    t0 = time.perf_counter()
-    got = oracle.keyswitch(ct, keys, q3, 3, LOG_N, 1, tables=tab3, per_ct_keys=True, threads=threads)
-    dt = time.perf_counter() - t0
     gpu_slice = out_t[: nb * 2 * 6 * N].cpu().numpy().view(np.uint64).reshape(nb, 2, 6, N)
-    out["keyswitch_parity"] = bool(np.array_equal(got, gpu_slice))
-    out["keyswitch"] = {"value": nb / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
-                        "sample": f"{nb} of the 64 N=16384 ciphertexts (dnum=3) with their own keys"}
-    # keyswitch at the reference shape (dnum = 6, the locked 60-bit primes):
-    # the sampled ciphertexts with their keys, parity against the GPU output
-    if "keyswitch_reference" in res and "_sample" in res["keyswitch_reference"]:
-        sm = res["keyswitch_reference"]["_sample"]
+    tab3 = oracle.Tables(q3, LOG_N)
+    got, dt = timed(lambda: oracle.keyswitch(ct, keys, q3, 3, LOG_N, 1, tables=tab3, per_ct_keys=True,
+                                             threads=threads))
+    got1, dt1 = timed(lambda: oracle.keyswitch(ct[:1], keys[:1], q3, 3, LOG_N, 1, tables=tab3, per_ct_keys=True,
+                                               threads=1))
+    out["keyswitch_parity"] = bool(np.array_equal(got, gpu_slice) and np.array_equal(got1, gpu_slice[:1]))
+    leg("keyswitch", nb / dt, "keyswitch/s", f"{nb} of the 64 N=16384 ciphertexts (dnum=3) with their own keys",
+        1 / dt1, "one of those ciphertexts, one thread")
+    # the rotation (Galois element 3) and the reference shape (dnum = 6, the
+    # locked 60-bit primes): the sampled ciphertexts with their keys
+    for name, dnum, g, what in (("keyswitch_rotation", 3, 3, "dnum=3, Galois element 3"),
+                                ("keyswitch_reference", 6, 1, "dnum=6, locked primes")):
+        if name not in res or "_sample" not in res[name]:
+            continue
+        sm = res[name]["_sample"]
         nb = sm["ct"].shape[0]
-        tab6 = oracle.Tables(sm["q"], LOG_N)
-        t0 = time.perf_counter()
-        got = oracle.keyswitch(sm["ct"], sm["keys"], sm["q"], 6, LOG_N, 1, tables=tab6, per_ct_keys=True,
-                               threads=threads)
-        dt = time.perf_counter() - t0
-        out["keyswitch_reference_parity"] = bool(np.array_equal(got, sm["out"]))
-        out["keyswitch_reference"] = {"value": nb / dt, "unit": "keyswitch/s", "cores": threads, "kind": "port",
-                                      "sample": f"{nb} of the 64 N=16384 ciphertexts (dnum=6, locked primes) "
-                                                "with their own keys"}
+        tb = oracle.Tables(sm["q"], LOG_N)
+        got, dt = timed(lambda: oracle.keyswitch(sm["ct"], sm["keys"], sm["q"], dnum, LOG_N, g, tables=tb,
+                                                 per_ct_keys=True, threads=threads))
+        got1, dt1 = timed(lambda: oracle.keyswitch(sm["ct"][:1], sm["keys"][:1], sm["q"], dnum, LOG_N, g, tables=tb,
+                                                   per_ct_keys=True, threads=1))
+        out[name + "_parity"] = bool(np.array_equal(got, sm["out"]) and np.array_equal(got1, sm["out"][:1]))
+        leg(name, nb / dt, "keyswitch/s", f"{nb} of the 64 N=16384 ciphertexts ({what}) with their own keys",
+            1 / dt1, "one of those ciphertexts, one thread")
     # GEMM: 64 rows of the 512x1024 activations against all 3072 weight rows
     x_t, w_t, y_t = res["gemm"]["_tensors"]
     rows = 64
     x = x_t[:rows].cpu().numpy().view(np.uint64)
     w = w_t.cpu().numpy()
-    t0 = time.perf_counter()
-    y = oracle.share_gemm(x, w, threads=threads)
-    dt = time.perf_counter() - t0
-    out["gemm_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
-    out["gemm"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
-                   "sample": f"{rows} of 512 activation rows x 1024 x 3072"}
+    yg = y_t[:rows].cpu().numpy().view(np.uint64)
+    y, dt = timed(lambda: oracle.share_gemm(x, w, threads=threads))
+    y1, dt1 = timed(lambda: oracle.share_gemm(x[:4], w, threads=1))
+    out["gemm_parity"] = bool(np.array_equal(y, yg) and np.array_equal(y1, yg[:4]))
+    leg("gemm", 2 * rows * 1024 * 3072 / dt / 1e12, "TOPS", f"{rows} of 512 activation rows x 1024 x 3072",
+        2 * 4 * 1024 * 3072 / dt1 / 1e12, "4 of those rows, one thread")
     # f12 GEMM: 16 activation rows against the int32 weights, parity with the
     # pre-split GPU product
     if "gemm_f12" in res and "_tensors" in res["gemm_f12"]:
@@ -423,12 +504,13 @@ def cpu_baselines(torch, res, budget_s: float):
         rows = 16
         x = x_t[:rows].cpu().numpy().view(np.uint64)
         w = w_t.cpu().numpy()
-        t0 = time.perf_counter()
-        y = oracle.share_gemm(x, w, threads=threads)
-        dt = time.perf_counter() - t0
-        out["gemm_f12_parity"] = bool(np.array_equal(y, y_t[:rows].cpu().numpy().view(np.uint64)))
-        out["gemm_f12"] = {"value": 2 * rows * 1024 * 3072 / dt / 1e12, "unit": "TOPS", "cores": threads,
-                           "kind": "port", "sample": f"{rows} of 512 activation rows x 1024 x 3072, int32 weights"}
+        yg = y_t[:rows].cpu().numpy().view(np.uint64)
+        y, dt = timed(lambda: oracle.share_gemm(x, w, threads=threads))
+        y1, dt1 = timed(lambda: oracle.share_gemm(x[:2], w, threads=1))
+        out["gemm_f12_parity"] = bool(np.array_equal(y, yg) and np.array_equal(y1, yg[:2]))
+        leg("gemm_f12", 2 * rows * 1024 * 3072 / dt / 1e12, "TOPS",
+            f"{rows} of 512 activation rows x 1024 x 3072, int32 weights",
+            2 * 2 * 1024 * 3072 / dt1 / 1e12, "2 of those rows, one thread")
     # token tile: two coordinates' columns (resident inputs transformed once,
     # as the GPU plan does at creation) and one level-0 merge, scaled to the
     # tile's 512 columns and 2,044 merges
@@ -441,59 +523,67 @@ def cpu_baselines(torch, res, budget_s: float):
         for x in qd:
             Q *= int(x)
         delta, r = [(Q >> 59) % int(x) for x in qd], Q & ((1 << 59) - 1)
-        t0 = time.perf_counter()
-        fins = []
-        for c in range(2):
+
+        def column(c, nthreads):
             ring = sm["rings"][c].view(np.uint64)
             scaled = oracle.local_dot_scale(sm["shares"], ring, delta, r, qd)
-            fins.append(oracle.token_finished(None, ring, scaled, qd, LOG_N, width, threads, resident=resident))
-        t_eval = (time.perf_counter() - t0) / 2
+            return oracle.token_finished(None, ring, scaled, qd, LOG_N, width, nthreads, resident=resident)
+
+        fins, t2 = timed(lambda: [column(c, threads) for c in range(2)])
+        t_eval = t2 / 2
         ok = all(np.array_equal(fins[c].reshape(-1), sm["finished"][c].view(np.uint64)) for c in range(2))
-        t0 = time.perf_counter()
-        pr = oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"], P, LOG_N,
-                              threads=threads)
-        t_pair = time.perf_counter() - t0
+        pr, t_pair = timed(lambda: oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"], P,
+                                                     LOG_N, threads=threads))
         ok &= bool(np.array_equal(pr.reshape(-1), sm["pair"].view(np.uint64)))
+        f1, t_eval1 = timed(lambda: column(0, 1))
+        pr1, t_pair1 = timed(lambda: oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"],
+                                                       P, LOG_N, threads=1))
+        ok &= bool(np.array_equal(f1, fins[0]) and np.array_equal(pr1, pr))
         coords, merges = res["token"]["coordinates"], res["token"]["merges_per_tile"]
-        tile_s = coords * t_eval + merges * t_pair
         out["token_parity"] = ok
-        out["token"] = {"value": coords / tile_s, "unit": "coordinates/s", "cores": threads, "kind": "port",
-                        "sample": f"2 of 512 columns ({slots} slots, {t_eval * 1e3:.0f} ms each) and one level-0 "
-                                  f"merge ({t_pair * 1e3:.0f} ms), scaled to 512 columns + {merges} merges"}
+        leg("token", coords / (coords * t_eval + merges * t_pair), "coordinates/s",
+            f"2 of 512 columns ({slots} slots, {t_eval * 1e3:.0f} ms each) and one level-0 merge "
+            f"({t_pair * 1e3:.0f} ms), scaled to 512 columns + {merges} merges",
+            coords / (coords * t_eval1 + merges * t_pair1),
+            f"one column ({t_eval1 * 1e3:.0f} ms) and one merge ({t_pair1 * 1e3:.0f} ms), one thread, scaled the same")
     # HE matrix product and encryption of zero: one evaluation each, with parity
     if "matrix" in res and "_sample" in res["matrix"]:
         sm = res["matrix"]["_sample"]
-        t0 = time.perf_counter()
-        want = oracle.matrix_product(sm["ct"], sm["ring"].view(np.uint64), sm["q"], LOG_N, threads=threads)
-        dt = time.perf_counter() - t0
-        out["matrix_parity"] = bool(np.array_equal(want.reshape(-1), sm["out"].view(np.uint64)))
-        out["matrix"] = {"value": 1 / dt, "unit": "evaluations/s", "cores": threads, "kind": "port",
-                         "sample": f"one evaluation ({res['matrix']['blocks']} blocks, N=16384, 6 primes), "
-                                   "inputs transformed inside the sample"}
+        ring = sm["ring"].view(np.uint64)
+        want, dt = timed(lambda: oracle.matrix_product(sm["ct"], ring, sm["q"], LOG_N, threads=threads))
+        want1, dt1 = timed(lambda: oracle.matrix_product(sm["ct"], ring, sm["q"], LOG_N, threads=1))
+        out["matrix_parity"] = bool(np.array_equal(want.reshape(-1), sm["out"].view(np.uint64))
+                                    and np.array_equal(want1, want))
+        leg("matrix", 1 / dt, "evaluations/s",
+            f"one evaluation ({res['matrix']['blocks']} blocks, N=16384, 6 primes), inputs transformed inside the "
+            "sample", 1 / dt1, "the same evaluation, one thread")
     if "enc0" in res and "_sample" in res["enc0"]:
         sm = res["enc0"]["_sample"]
-        t0 = time.perf_counter()
-        want = oracle.enc0(sm["samples"].view(np.uint64).reshape(3, 7, N), sm["pk"].view(np.uint64), sm["q"], LOG_N,
-                           threads=threads)
-        dt = time.perf_counter() - t0
-        out["enc0_parity"] = bool(np.array_equal(want.reshape(-1), sm["out"].view(np.uint64)))
-        out["enc0"] = {"value": 1 / dt, "unit": "encryptions/s", "cores": threads, "kind": "port",
-                       "sample": "one encryption of zero (N=16384, 6 + 1 primes)"}
+        smp = sm["samples"].view(np.uint64).reshape(3, 7, N)
+        want, dt = timed(lambda: oracle.enc0(smp, sm["pk"].view(np.uint64), sm["q"], LOG_N, threads=threads))
+        want1, dt1 = timed(lambda: oracle.enc0(smp, sm["pk"].view(np.uint64), sm["q"], LOG_N, threads=1))
+        out["enc0_parity"] = bool(np.array_equal(want.reshape(-1), sm["out"].view(np.uint64))
+                                  and np.array_equal(want1, want))
+        leg("enc0", 1 / dt, "encryptions/s", "one encryption of zero (N=16384, 6 + 1 primes)",
+            1 / dt1, "the same encryption, one thread")
     # Qwen3: the four products of layer 0 on 16 of the 512 token rows
     if "qwen3" in res and "_sample" in res["qwen3"]:
-        ok, ops, dt = True, 0, 0.0
+        ok, ops, ops1, dt, dt1 = True, 0, 0, 0.0, 0.0
         for x_t, w_t, sh_t, y_t in res["qwen3"]["_sample"]:
             x = x_t.numpy().view(np.uint64)
             w = w_t.numpy()
             sh = None if sh_t is None else sh_t.numpy()
-            t0 = time.perf_counter()
-            y = oracle.share_gemm(x, w, sh, mask_bits=64, threads=threads)
-            dt += time.perf_counter() - t0
+            yg = y_t.numpy().view(np.uint64)
+            y, t = timed(lambda: oracle.share_gemm(x, w, sh, mask_bits=64, threads=threads))
+            y1, t1 = timed(lambda: oracle.share_gemm(x[:2], w, sh, mask_bits=64, threads=1))
+            dt, dt1 = dt + t, dt1 + t1
             ops += 2 * x.shape[0] * x.shape[1] * w.shape[0]
-            ok &= bool(np.array_equal(y, y_t.numpy().view(np.uint64)))
+            ops1 += 2 * 2 * x.shape[1] * w.shape[0]
+            ok &= bool(np.array_equal(y, yg) and np.array_equal(y1, yg[:2]))
         out["qwen3_parity"] = ok
-        out["qwen3"] = {"value": ops / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
-                        "sample": "layer 0, 16 of 512 token rows, all four products (q|k|v, o, gate|up, down)"}
+        leg("qwen3", ops / dt / 1e12, "TOPS",
+            "layer 0, 16 of 512 token rows, all four products (q|k|v, o, gate|up, down)",
+            ops1 / dt1 / 1e12, "2 of those rows, one thread")
     return out
 
 
@@ -502,7 +592,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "keyswitch_dnum3", "keyswitch_dnum6", "gemm",
+    ap.add_argument("--only", choices=["all", "ntt", "keyswitch", "keyswitch_dnum3", "keyswitch_rotation",
+                                       "keyswitch_dnum6", "gemm",
                                        "gemm_f12", "qwen3", "token", "matrix", "enc0", "copy"],
                     default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle CPU baselines")
@@ -533,6 +624,18 @@ def main() -> int:
         log("keyswitch N=16384 dnum=3, 64 ciphertexts ...")
         res["keyswitch"] = bench_keyswitch(torch, praghip, args.steps, args.warmup)
         log(f"keyswitch {res['keyswitch']['keyswitch_per_s']:.4g}/s")
+    if args.only in ("all", "keyswitch", "keyswitch_rotation"):
+        log("keyswitch N=16384 dnum=3, Galois element 3 (rotation), 64 ciphertexts ...")
+        res["keyswitch_rotation"] = bench_keyswitch(torch, praghip, args.steps, args.warmup, galois=3)
+        ct_t, keys_t, out_t, q3 = res["keyswitch_rotation"].pop("_tensors")
+        if not args.no_cpu and args.only == "all":
+            nb, cw, kw = 4, 2 * 6 * N, 3 * 2 * 7 * N
+            host = lambda t, w: t[: nb * w].cpu().numpy().view(np.uint64).copy()  # noqa: E731
+            res["keyswitch_rotation"]["_sample"] = {"ct": host(ct_t, cw).reshape(nb, 2, 6, N),
+                                                    "keys": host(keys_t, kw).reshape(nb, 3, 2, 7, N),
+                                                    "out": host(out_t, cw).reshape(nb, 2, 6, N), "q": q3}
+        del ct_t, keys_t, out_t
+        log(f"keyswitch (rotation) {res['keyswitch_rotation']['keyswitch_per_s']:.4g}/s")
     if args.only in ("all", "keyswitch", "keyswitch_dnum6"):
         log("keyswitch N=16384 dnum=6, locked 60-bit primes (the reference shape), 64 ciphertexts ...")
         res["keyswitch_reference"] = bench_keyswitch(torch, praghip, args.steps, args.warmup, reference=True)
@@ -594,15 +697,17 @@ def main() -> int:
     def clean(d):
         return {k: v for k, v in d.items() if not k.startswith("_")}
 
-    key = next(k for k in ("ntt", "keyswitch", "keyswitch_reference", "gemm", "gemm_f12", "qwen3", "token", "matrix",
-                           "enc0") if k in res)
+    key = next(k for k in ("ntt", "keyswitch", "keyswitch_rotation", "keyswitch_reference", "gemm", "gemm_f12",
+                           "qwen3", "token", "matrix", "enc0") if k in res)
     primary = res[key]
     value = {"ntt": lambda r: r["ntt_per_s"], "keyswitch": lambda r: r["keyswitch_per_s"],
              "keyswitch_reference": lambda r: r["keyswitch_per_s"],
+             "keyswitch_rotation": lambda r: r["keyswitch_per_s"],
              "gemm": lambda r: r["tops"], "gemm_f12": lambda r: r["tops"], "qwen3": lambda r: r["tops"],
              "token": lambda r: r["coordinates_per_s"], "matrix": lambda r: r["evaluations_per_s"],
              "enc0": lambda r: r["encryptions_per_s"]}[key](primary)
-    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "keyswitch_reference": "keyswitch/s", "gemm": "TOPS",
+    unit = {"ntt": "limb-NTT/s", "keyswitch": "keyswitch/s", "keyswitch_reference": "keyswitch/s",
+            "keyswitch_rotation": "keyswitch/s", "gemm": "TOPS",
             "gemm_f12": "TOPS", "qwen3": "TOPS",
             "token": "coordinates/s", "matrix": "evaluations/s", "enc0": "encryptions/s"}[key]
     line = {
@@ -624,6 +729,8 @@ def main() -> int:
             "keyswitch": "keyswitch N=16384 L=6 (+1 special prime), dnum=3, 64 ciphertexts, 64 keys",
             "keyswitch_reference": "keyswitch N=16384, six locked 60-bit primes + special, dnum=6, 64 ciphertexts, "
                                    "64 keys",
+            "keyswitch_rotation": "keyswitch N=16384 L=6 (+1 special prime), dnum=3, Galois element 3, "
+                                  "64 ciphertexts, 64 keys",
             "gemm": "share GEMM u64[512x1024] x int8[3072x1024]^T mod 2^64",
             "gemm_f12": "share GEMM u64[512x1024] x int32 f12[3072x1024]^T mod 2^64 (pre-split weights)",
             "qwen3": "Qwen3-0.6B local share GEMMs, 28 layers x 4 products, 512 tokens",
