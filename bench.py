@@ -40,6 +40,7 @@ LOG_N = 14
 TRAFFIC_SOURCES = {
     "ntt": ("ntt_n16384_3072limbs.md", r"ntt_kernel<14,", 2),
     "keyswitch": ("keyswitch_n16384_L6_dnum3_batch64.md", r"ks_", 1),
+    "keyswitch_rotation": ("keyswitch_n16384_L6_dnum3_rotation_batch64.md", r"ks_", 1),
     "keyswitch_reference": ("keyswitch_n16384_locked_dnum6_batch64.md", r"ks_", 1),
     "gemm": ("share_gemm_512x1024x3072_i8.md", r"share_gemm_dma_kernel", 1),
     "gemm_f12": ("share_gemm_512x1024x3072_f12.md", r"share_gemm_dma_kernel|gemm_clear_kernel", 1),
@@ -181,7 +182,8 @@ def bench_keyswitch(torch, praghip, steps, warmup, reference=False, galois=1):
         "batch": batch, "dnum": dnum, "galois": galois, "ms_per_step": ms, "keyswitch_per_s": batch / (ms * 1e-3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None if galois != 1 else measured_traffic("keyswitch_reference" if reference else "keyswitch"),
+                     "traffic": measured_traffic("keyswitch_reference" if reference else
+                                                 ("keyswitch" if galois == 1 else "keyswitch_rotation")),
                      "kernel": "whole keyswitch batch (all its launches); traffic is per batch",
                      "algorithmic_bytes_per_batch": batch * bytes_per_ks,
                      "algorithmic_bytes_per_keyswitch": bytes_per_ks},
@@ -532,12 +534,17 @@ def cpu_baselines(torch, res, budget_s: float):
         fins, t2 = timed(lambda: [column(c, threads) for c in range(2)])
         t_eval = t2 / 2
         ok = all(np.array_equal(fins[c].reshape(-1), sm["finished"][c].view(np.uint64)) for c in range(2))
-        pr, t_pair = timed(lambda: oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"], P,
-                                                     LOG_N, threads=threads))
+        tk = oracle.Tables(sm["q"], LOG_N)
+
+        def merge(nthreads):
+            return oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"], P, LOG_N,
+                                    tables=tk, threads=nthreads)
+
+        merge(threads)  # first call outside the timing (thread pool start-up)
+        pr, t_pair = timed(lambda: merge(threads))
         ok &= bool(np.array_equal(pr.reshape(-1), sm["pair"].view(np.uint64)))
         f1, t_eval1 = timed(lambda: column(0, 1))
-        pr1, t_pair1 = timed(lambda: oracle.pack_pair(fins[0][0], fins[1][0], 0, sm["keys"].view(np.uint64), sm["q"],
-                                                       P, LOG_N, threads=1))
+        pr1, t_pair1 = timed(lambda: merge(1))
         ok &= bool(np.array_equal(f1, fins[0]) and np.array_equal(pr1, pr))
         coords, merges = res["token"]["coordinates"], res["token"]["merges_per_tile"]
         out["token_parity"] = ok
@@ -629,7 +636,7 @@ def main() -> int:
         res["keyswitch_rotation"] = bench_keyswitch(torch, praghip, args.steps, args.warmup, galois=3)
         ct_t, keys_t, out_t, q3 = res["keyswitch_rotation"].pop("_tensors")
         if not args.no_cpu and args.only == "all":
-            nb, cw, kw = 4, 2 * 6 * N, 3 * 2 * 7 * N
+            nb, cw, kw = 16, 2 * 6 * N, 3 * 2 * 7 * N
             host = lambda t, w: t[: nb * w].cpu().numpy().view(np.uint64).copy()  # noqa: E731
             res["keyswitch_rotation"]["_sample"] = {"ct": host(ct_t, cw).reshape(nb, 2, 6, N),
                                                     "keys": host(keys_t, kw).reshape(nb, 3, 2, 7, N),
