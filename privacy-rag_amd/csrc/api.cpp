@@ -21,7 +21,9 @@
 
 namespace praghip {
 hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
-                             int M, int K, int N, int mask_bits, hipStream_t s);
+                             int M, int K, int N, int mask_bits, hipStream_t s, bool y_zero = false);
+bool share_gemm_adds_into_y(const void* x, const void* w, int w_bits, int M, int K, int N);
+hipError_t launch_gemm_clear_list(const GemmClearList& l, hipStream_t s);
 hipError_t launch_weight_split(const int32_t* w, int8_t* planes, size_t count, hipStream_t s);
 hipError_t launch_share_gemm_valu(const uint64_t* x, const int8_t* w, const int8_t* shifts, uint64_t* y, int M,
                                   int K, int N, int mask_bits, hipStream_t s);
@@ -936,13 +938,51 @@ int praghip_share_gemm_batch(int device, const praghip_gemm_desc* list, size_t c
         (d.w_bits == 32 && (reinterpret_cast<uintptr_t>(d.w) & 3)))
       return fail(PRAGHIP_E_ARGUMENT, "E_SHARE_ALIGNMENT");
   }
+  // the outputs that split-K products add into are zeroed together, one
+  // launch per up to kGemmClearMax of them, when none of them overlaps any
+  // other operand of the batch (an earlier product could read it); otherwise
+  // each product clears its own output just before it runs
+  std::vector<size_t> adds;
+  for (size_t i = 0; i < count; ++i) {
+    const praghip_gemm_desc& d = list[i];
+    if (d.m && d.n && share_gemm_adds_into_y(d.x, d.w, d.w_bits, int(d.m), int(d.k), int(d.n))) adds.push_back(i);
+  }
+  const auto span = [](const void* p, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return std::pair<uintptr_t, uintptr_t>(a, a + bytes);
+  };
+  const auto overlaps = [](std::pair<uintptr_t, uintptr_t> a, std::pair<uintptr_t, uintptr_t> b) {
+    return a.first < b.second && b.first < a.second;
+  };
+  bool together = adds.size() > 1;
+  for (size_t a = 0; a < adds.size() && together; ++a) {
+    const praghip_gemm_desc& da = list[adds[a]];
+    const auto ya = span(da.y, da.m * da.n * 8);
+    for (size_t j = 0; j < count && together; ++j) {
+      const praghip_gemm_desc& d = list[j];
+      if (!d.m || !d.n) continue;
+      const size_t wbytes = d.n * d.k * (d.w_bits == 8 ? 1 : d.w_bits == 24 ? 3 : 4);
+      if (overlaps(ya, span(d.x, d.m * d.k * 8)) || overlaps(ya, span(d.w, wbytes)) ||
+          (d.shifts && overlaps(ya, span(d.shifts, d.n))) || (j != adds[a] && overlaps(ya, span(d.y, d.m * d.n * 8))))
+        together = false;
+    }
+  }
   DeviceScope scope(device);
   hipError_t e = scope.status();
+  if (together)
+    for (size_t a0 = 0; a0 < adds.size() && e == hipSuccess; a0 += kGemmClearMax) {
+      GemmClearList l{};
+      for (size_t a = a0; a < adds.size() && l.count < kGemmClearMax; ++a) {
+        l.ptr[l.count] = list[adds[a]].y;
+        l.words[l.count++] = list[adds[a]].m * list[adds[a]].n;
+      }
+      e = launch_gemm_clear_list(l, static_cast<hipStream_t>(stream));
+    }
   for (size_t i = 0; i < count && e == hipSuccess; ++i) {
     const praghip_gemm_desc& d = list[i];
     if (d.m == 0 || d.n == 0) continue;
     e = launch_share_gemm(d.x, d.w, d.w_bits, d.shifts, d.y, int(d.m), int(d.k), int(d.n), d.mask_bits,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<hipStream_t>(stream), together);
   }
   if (e != hipSuccess) return fail(PRAGHIP_E_DEVICE, std::string("E_SHARE_HIP: ") + hipGetErrorString(e));
   return PRAGHIP_OK;

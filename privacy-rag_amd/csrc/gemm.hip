@@ -744,8 +744,36 @@ hipError_t launch_weight_split(const int32_t* w, int8_t* planes, size_t count, h
   return hipGetLastError();
 }
 
+// Zero several outputs in one launch (a batch's split-K products): blockIdx.y
+// names the buffer.
+__global__ void __launch_bounds__(256) gemm_clear_list_kernel(GemmClearList l) {
+  uint64_t* y = l.ptr[blockIdx.y];
+  const size_t n = l.words[blockIdx.y];
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) y[i] = 0;
+}
+
+hipError_t launch_gemm_clear_list(const GemmClearList& l, hipStream_t s) {
+  if (l.count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gemm_clear_list_kernel, dim3(512, unsigned(l.count)), dim3(256), 0, s, l);
+  return hipGetLastError();
+}
+
+// Split-K products add their partial products into y with atomics, so y must
+// be zero first; true when this product takes that path.
+bool share_gemm_adds_into_y(const void* x, const void* w, int w_bits, int M, int K, int N) {
+  if (w_bits != 8 && w_bits != 24) return false;
+  const int w_vec = (K % 16 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+  if (!(K % kBK == 0 && w_vec && reinterpret_cast<uintptr_t>(x) % 16 == 0)) return false;
+  const int planes = w_bits == 8 ? 1 : 3, ksteps = K / kBK;
+  const long tiles2 = long((N + 127) / 128) * long((M + kBM - 1) / kBM);
+  int splits = 1;
+  while (splits < 4 && tiles2 * splits < 256 && ksteps / (splits * 2) >= 8) splits *= 2;
+  const int k_split = (ksteps + splits - 1) / splits * kBK;
+  return ((K + k_split - 1) / k_split) * planes > 1;
+}
+
 hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const int8_t* shifts, uint64_t* y,
-                             int M, int K, int N, int mask_bits, hipStream_t s) {
+                             int M, int K, int N, int mask_bits, hipStream_t s, bool y_zero) {
   const uint64_t mask = mask_bits >= 64 ? ~0ull : ((1ull << mask_bits) - 1);
   const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(kThreads);
   // 16-byte weight loads need 16-byte aligned rows
@@ -773,7 +801,7 @@ hipError_t launch_share_gemm(const uint64_t* x, const void* w, int w_bits, const
       const unsigned fgrid = unsigned(std::min<size_t>((words + 255) / 256, 4096));
       // several planes or K splits add their partial products into y
       const bool atomic = splits * planes > 1;
-      if (atomic) {
+      if (atomic && !y_zero) {
         hipLaunchKernelGGL(gemm_clear_kernel, dim3(fgrid), dim3(256), 0, s, y, words, 0ull);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -167,4 +167,13 @@ hipError_t launch_keyswitch_rows(const KsArgs& a, const KsConst* kc_dev, const K
 // Ciphertexts per three-phase chunk a plan sizes its `inter` scratch for.
 constexpr size_t kKsRowsChunk = 64;
 
+// Outputs a batched share GEMM zeroes in one launch before its split-K
+// products (launch_gemm_clear_list, gemm.hip).
+constexpr int kGemmClearMax = 64;
+struct GemmClearList {
+  uint64_t* ptr[kGemmClearMax];
+  size_t words[kGemmClearMax];
+  int count;
+};
+
 }  // namespace praghip

@@ -147,3 +147,54 @@ def test_gemm_valu_form(gpu, m, k, n):
         y = praghip.share_gemm_valu(to_dev(x), torch.from_numpy(w).cuda(), shifts=ts, mask_bits=mask)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(from_dev(y), oracle.share_gemm(x, w, shifts, mask))
+
+
+def _batch(descs):
+    import ctypes
+
+    import torch
+    from praghip import _lib
+    arr = (_lib.GemmDesc * len(descs))(*[
+        _lib.GemmDesc(x.data_ptr(), w.data_ptr(), 0 if s is None else s.data_ptr(), y.data_ptr(), x.shape[0],
+                      x.shape[1], w.shape[0], 8, mask) for x, w, s, y, mask in descs])
+    _lib.check(_lib.lib().praghip_share_gemm_batch(0, ctypes.cast(arr, ctypes.c_void_p), len(descs), None))
+    torch.cuda.synchronize()
+
+
+def test_gemm_batch_split_k_outputs_cleared_together(gpu):
+    """praghip_share_gemm_batch zeroes the outputs of its split-K products in
+    one launch before the first product (the Qwen3 o and down shapes here,
+    with and without the 59-bit mask), and falls back to a clear per product
+    when such an output is also an earlier product's input: product 1 reads
+    buffer B as its shares, then product 2 (split K) writes B."""
+    import torch
+    specs = [(512, 2048, 1024, None, 64), (512, 3072, 1024, 7001, 59), (64, 1024, 512, None, 64),
+             (512, 2048, 1024, 7002, 64)]
+    descs, want = [], []
+    for i, (m, k, n, shseed, mask) in enumerate(specs):
+        x = oracle.fill_u64(m * k, 8000 + i).reshape(m, k)
+        w = oracle.fill_i8(n * k, 8100 + i).reshape(n, k)
+        sh = None if shseed is None else oracle.fill_shift(n, shseed)
+        want.append(oracle.share_gemm(x, w, sh, mask))
+        ts = None if sh is None else torch.from_numpy(sh.astype(np.int8)).cuda()
+        y = to_dev(np.full((m, n), 0x1234, dtype=np.uint64))  # stale values the clear must remove
+        descs.append((to_dev(x), torch.from_numpy(w).cuda(), ts, y, mask))
+    print("[gemm] batch, outputs cleared together", flush=True)
+    _batch(descs)
+    for i, d in enumerate(descs):
+        np.testing.assert_array_equal(from_dev(d[3]), want[i], err_msg=f"product {i}")
+    # overlap: product 1's shares are B, product 2 (split K, [512 x 1024]) writes B
+    m, k, n = 512, 1024, 1024
+    xb = oracle.fill_u64(m * k, 8200).reshape(m, k)
+    w1 = oracle.fill_i8(512 * k, 8201).reshape(512, k)
+    x2 = oracle.fill_u64(m * 2048, 8202).reshape(m, 2048)
+    w2 = oracle.fill_i8(n * 2048, 8203).reshape(n, 2048)
+    B = to_dev(xb)
+    y1 = to_dev(np.zeros((m, 512), dtype=np.uint64))
+    y0 = to_dev(np.zeros((m, n), dtype=np.uint64))
+    tw1, tw2, tx2 = torch.from_numpy(w1).cuda(), torch.from_numpy(w2).cuda(), to_dev(x2)
+    print("[gemm] batch, split-K output overlapping an earlier input", flush=True)
+    _batch([(tx2, tw2, None, y0, 64), (B, tw1, None, y1, 64), (tx2, tw2, None, B, 64)])
+    np.testing.assert_array_equal(from_dev(y1), oracle.share_gemm(xb, w1))
+    np.testing.assert_array_equal(from_dev(B), oracle.share_gemm(x2, w2))
+    np.testing.assert_array_equal(from_dev(y0), oracle.share_gemm(x2, w2))
