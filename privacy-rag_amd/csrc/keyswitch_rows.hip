@@ -60,6 +60,7 @@ template <class A>
 struct TypeTag {
   using type = A;
 };
+typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint64_t bits_of(double x) { return (uint64_t)__double_as_longlong(x); }
 __device__ __forceinline__ double double_of(uint64_t x) { return __longlong_as_double((long long)x); }
@@ -378,7 +379,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1
 // exchange buffer: six items fit a CU's 160 KiB), so the digits' passes issue
 // no vector-memory loads, and the next digit's row and this digit's key words
 // are in flight while the passes run (vector loads complete in order: a
-// twiddle load behind them would wait for them).
+// twiddle load behind them would wait for them).  E and the keys are read
+// with nontemporal loads: each of their words is read once, and streamed
+// through L2 as ordinary loads they evict the twiddle tables that every
+// item's copy reads.
 constexpr int kRowLE = 3;                           // 8 coefficients per lane
 constexpr unsigned kRow2Threads = 1u << (kRowLog - kRowLE);  // 128: the item's two waves
 
@@ -524,7 +528,7 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
   row_twiddles_fill(ltw, fwd_table<A>(f, int(t)), row, t2);
   uint64_t en[E];
 #pragma unroll
-  for (int k = 0; k < E; ++k) en[k] = e0[fwd_in_index<kRowLog, kRowLE>(t2, k)];
+  for (int k = 0; k < E; ++k) en[k] = __builtin_nontemporal_load(&e0[fwd_in_index<kRowLog, kRowLE>(t2, k)]);
   __syncthreads();
   T a0[E], a1[E];
   if constexpr (kMont) {
@@ -538,7 +542,7 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
     if (j + 1 < dnum) {  // the next digit's row, in flight during this digit's passes
       const uint64_t* src = e0 + (j + 1) * e_step;
 #pragma unroll
-      for (int k = 0; k < E; ++k) en[k] = src[fwd_in_index<kRowLog, kRowLE>(t2, k)];
+      for (int k = 0; k < E; ++k) en[k] = __builtin_nontemporal_load(&src[fwd_in_index<kRowLog, kRowLE>(t2, k)]);
     }
     // the digit's key words, issued at the start of forward pass kRowKeyPass:
     // registers r, r + 1 hold adjacent coefficients after the last forward
@@ -550,8 +554,10 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
 #pragma unroll
       for (int r = 0; r < E; r += 2) {
         const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog, kRowLE>(t2, r);
-        kav[r / 2] = *reinterpret_cast<const ulonglong2*>(k0 + pos);
-        kkv[r / 2] = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+        const u64x2 a = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(k0 + pos));
+        const u64x2 c = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(k1 + pos));
+        kav[r / 2] = make_ulonglong2(a.x, a.y);
+        kkv[r / 2] = make_ulonglong2(c.x, c.y);
       }
     });
 #pragma unroll
