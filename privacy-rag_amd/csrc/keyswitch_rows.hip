@@ -681,14 +681,17 @@ __device__ __forceinline__ NttPrime product_prime(const KsRows& f, const KsConst
   return r;
 }
 
-// Canonical coefficient-form residues of one product limb at column c.
+// Canonical coefficient-form residues of one product limb at column c (a
+// limb each thread reads once: nontemporal loads, as for the ModDown's own
+// limb and its output below, so that these streams leave L2 to the special
+// prime's rounding term that every data prime of a column reads).
 template <class A>
 __device__ __forceinline__ void column_residues(uint64_t (&x)[kE], const uint64_t* __restrict__ src,
                                                 const typename A::TW* __restrict__ tab, const NttPrime& pr) {
   const A ar(pr);
   typename A::T v[kE];
 #pragma unroll
-  for (int k = 0; k < kE; ++k) v[k] = load_form<A>(src[unsigned(k) << kRowLog]);
+  for (int k = 0; k < kE; ++k) v[k] = load_form<A>(__builtin_nontemporal_load(&src[unsigned(k) << kRowLog]));
   top_inv<A>(v, tab, ar, pr);
 #pragma unroll
   for (int k = 0; k < kE; ++k) x[k] = ar.to_u64_inv(v[k]);
@@ -743,7 +746,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(std::i
       double v[kE];
       uint64_t lastv[kE], c0v[kE];
 #pragma unroll
-      for (int k = 0; k < kE; ++k) v[k] = double_of(pc[(size_t(i) << kLog) + (unsigned(k) << kRowLog)]);
+      for (int k = 0; k < kE; ++k) v[k] = double_of(__builtin_nontemporal_load(&pc[(size_t(i) << kLog) + (unsigned(k) << kRowLog)]));
 #pragma unroll
       for (int k = 0; k < kE; ++k) lastv[k] = pc[(size_t(L) << kLog) + (unsigned(k) << kRowLog)];
       if (comp == 0) {
@@ -762,7 +765,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(std::i
         const double red = mul_f64(double(last >> 32), c32, c32q, pi.qd) + double(last & 0xffffffffull);
         double r = mul_f64(reduce_f64(v[k], pi.qd, pi.qinv) - red + half, ip, ipq, pi.qd);  // |r| < 1.8 q
         r += ArF64::from_u64(c0v[k]);
-        o[unsigned(k) << kRowLog] = ar.to_u64(r);
+        __builtin_nontemporal_store(ar.to_u64(r), &o[unsigned(k) << kRowLog]);
       }
       return;
     }
@@ -777,7 +780,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(std::i
     const uint64_t corr = sub_mod(reduced, kc.half_mod[i], qi);
     uint64_t val = mul_shoup(sub_mod(x[k], corr, qi), kc.invp[i].w, kc.invp[i].wq, qi);
     if (comp == 0) val = add_mod(val, c0v[k], qi);
-    o[unsigned(k) << kRowLog] = val;
+    __builtin_nontemporal_store(val, &o[unsigned(k) << kRowLog]);
   }
 }
 
