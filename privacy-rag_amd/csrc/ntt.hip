@@ -17,9 +17,10 @@ namespace praghip {
 // transformed in registers + LDS and stored in the last pass's layout.  The
 // float-path forward kernel issues the next limb's loads as soon as the
 // current limb no longer needs the LDS (before its last pass), so they overlap
-// the last pass and the stores instead of starting after them; the other
-// kernels have no registers to spare for them and load each limb at the top
-// of its turn.
+// the last pass and the stores instead of starting after them.  The
+// float-path inverse kernel loads the next limb's first-pass twiddles before
+// the current limb's stores and its words after them; the other kernels have
+// no registers to spare and load each limb at the top of its turn.
 //
 // LIFT (forward only): limb l = b P + k is not read from data but formed on
 // load from ring block b, lift59_residue mod q_k (ring[b][z] when width = 0;
@@ -97,6 +98,35 @@ __global__ void __launch_bounds__(ntt_threads<LOGN>())
         if (vn < count) load(raw, limb_of(vn));
       });
       store(ar, x, limb);
+    }
+  } else if constexpr (std::is_same<T, double>::value && INV) {
+    // the next limb's first-pass twiddles are loaded before this limb's
+    // stores (vector memory operations complete in order: issued behind the
+    // stores they would wait for them, and the first pass waits for its
+    // twiddles); its words after them (before the stores as well, they cost
+    // registers and measured no faster)
+    size_t v = blockIdx.x;
+    if (v >= count) return;
+    uint64_t raw[kE];
+    typename A::TW w0[pass_twiddles<Passes<LOGN>::r(INV, 0)>()];
+    {
+      const size_t limb = limb_of(v);
+      load(raw, limb);
+      load_pass_twiddles<LOGN, INV, 0>(w0, t, tw + ((limb % unsigned(P)) << LOGN));
+    }
+    for (; v < count; v += gridDim.x) {
+      const size_t limb = limb_of(v);
+      const int p = int(limb % unsigned(P));
+      const NttPrime pr = primes[p];
+      const A ar(pr);
+      T x[kE];
+#pragma unroll
+      for (int j = 0; j < kE; ++j) x[j] = ar.from_u64(raw[j]);
+      run_passes<LOGN, INV, 0>(x, reinterpret_cast<T*>(lds), t, tw + (size_t(p) << LOGN), ar, pr, w0, [] {});
+      const size_t vn = v + gridDim.x;
+      if (vn < count) load_pass_twiddles<LOGN, INV, 0>(w0, t, tw + ((limb_of(vn) % unsigned(P)) << LOGN));
+      store(ar, x, limb);
+      if (vn < count) load(raw, limb_of(vn));
     }
   } else {
     for (size_t v = blockIdx.x; v < count; v += gridDim.x) {

@@ -511,10 +511,17 @@ __device__ __forceinline__ void exchange(T (&v)[E], T* lds, unsigned t) {
   const T* rbase = lds + lds_pos(B::elem(t, 0));
 #pragma unroll
   for (int j = 0; j < (1 << LE); ++j) v[j] = rbase[B::slot_offset(j)];
-  if constexpr (in_wave)
+  if constexpr (in_wave) {
     __builtin_amdgcn_wave_barrier();
-  else
+  } else {
     __syncthreads();
+    // The compiler does not count s_barrier as a memory access when it sinks
+    // loads into a successor block: where the values read here are first used
+    // after a branch, it moved these LDS reads below the barrier, where a
+    // faster wave's next LDS writes can overwrite what they read.  An empty asm
+    // with a memory clobber does count, and pins the reads above it.
+    asm volatile("" ::: "memory");
+  }
 }
 
 // Pass P with its twiddles already in registers; loads pass P+1's twiddles

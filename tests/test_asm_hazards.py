@@ -16,6 +16,15 @@ these two kinds against the last writer of its register:
   the compiler leaves exactly that for its own code (s_nop 1, or s_nop 0 plus
   one instruction), so the same rule checks the asm and the compiler alike;
 * a write of M0 is followed by at least one wait state before an LDS DMA.
+
+A third check covers the LDS exchanges between transform passes (barrier,
+writes, barrier, reads, barrier).  The compiler does not count s_barrier as
+a memory access when it sinks loads into a successor block: with the values
+read first used after a branch, it once moved an exchange's reads below the
+barrier that follows them (a faster wave's next writes then raced them).
+The exchange now pins its reads with an empty asm memory clobber; the test
+checks that every barrier ending a run of LDS writes is followed by LDS reads
+before the next barrier.
 """
 import os
 import re
@@ -195,4 +204,35 @@ def test_m0_write_precedes_lds_dma_by_one_wait_state(machine_code):
             bad += 1
             worst.append((machine_code[w[2]][2], line))
     assert dmas > 0  # the share GEMM's DMA kernel
+    assert bad == 0, worst[:5]
+
+
+def test_exchange_reads_stay_between_barriers(machine_code):
+    """Barrier, LDS writes, barrier, LDS reads, barrier: the reads stay before
+    the third barrier (straight-line code; a branch ends the run)."""
+    exchanges = bad = 0
+    worst = []
+    after_writes = False  # the last barrier ended a run of LDS writes
+    last_lds = None
+    func = None
+    for op, ops, line in machine_code:
+        if op == "FUNC":
+            func, after_writes, last_lds = line, False, None
+            continue
+        if block_start(op):
+            after_writes, last_lds = False, None
+            continue
+        if op.startswith("ds_"):
+            kind = "r" if "read" in op else ("w" if "write" in op else "o")
+            if after_writes and kind == "r":
+                after_writes = False
+                exchanges += 1
+            last_lds = kind
+        elif op == "s_barrier":
+            if after_writes:
+                bad += 1
+                worst.append(func)
+            after_writes = last_lds == "w"
+            last_lds = None
+    assert exchanges > 50  # the transforms' cross-wave exchanges
     assert bad == 0, worst[:5]
