@@ -379,10 +379,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 1
 // exchange buffer: six items fit a CU's 160 KiB), so the digits' passes issue
 // no vector-memory loads, and the next digit's row and this digit's key words
 // are in flight while the passes run (vector loads complete in order: a
-// twiddle load behind them would wait for them).  E and the keys are read
-// with nontemporal loads: each of their words is read once, and streamed
-// through L2 as ordinary loads they evict the twiddle tables that every
-// item's copy reads.
+// twiddle load behind them would wait for them).  E is read with
+// nontemporal loads, and so are the keys when every ciphertext has its own:
+// each of those words is read once, and streamed through L2 as ordinary
+// loads they evict the twiddle tables that every item's copy reads (a key
+// shared by a batch is re-read by its other items and stays cached).
 constexpr int kRowLE = 3;                           // 8 coefficients per lane
 constexpr unsigned kRow2Threads = 1u << (kRowLog - kRowLE);  // 128: the item's two waves
 
@@ -520,6 +521,7 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
   const A ar(pr);
   const typename A::TW* ti = inv_table<A>(f, int(t));
   const uint64_t* kb = f.key + size_t(b / f.key_group) * f.key_stride + (size_t(t) << kLog);
+  const bool own_keys = f.key_group == 1;  // shared keys are re-read by other items: leave them cached
   const uint64_t* e0 = f.e + (size_t(bl) * dnum * K + t) * kN + (row << kRowLog);
   const size_t e_step = size_t(K) * kN;  // digit to digit in E
   // the row's forward twiddles into LDS, then the first digit's row (the
@@ -554,10 +556,15 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
 #pragma unroll
       for (int r = 0; r < E; r += 2) {
         const unsigned pos = (row << kRowLog) | fwd_out_index<kRowLog, kRowLE>(t2, r);
-        const u64x2 a = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(k0 + pos));
-        const u64x2 c = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(k1 + pos));
-        kav[r / 2] = make_ulonglong2(a.x, a.y);
-        kkv[r / 2] = make_ulonglong2(c.x, c.y);
+        if (own_keys) {
+          const u64x2 a = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(k0 + pos));
+          const u64x2 c = __builtin_nontemporal_load(reinterpret_cast<const u64x2*>(k1 + pos));
+          kav[r / 2] = make_ulonglong2(a.x, a.y);
+          kkv[r / 2] = make_ulonglong2(c.x, c.y);
+        } else {
+          kav[r / 2] = *reinterpret_cast<const ulonglong2*>(k0 + pos);
+          kkv[r / 2] = *reinterpret_cast<const ulonglong2*>(k1 + pos);
+        }
       }
     });
 #pragma unroll
