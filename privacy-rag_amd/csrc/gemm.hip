@@ -546,12 +546,15 @@ __device__ __forceinline__ void piped_step(const DmaCtx& c, int s, int steps, in
   interleave_half<CB>();
 }
 
-// The other half of the wave's value (lane l ^ 32), 64 bits.
-__device__ __forceinline__ uint64_t swap_halves(uint64_t v, int lane) {
-  const int addr = (lane ^ 32) << 2;
-  const uint32_t lo = uint32_t(__builtin_amdgcn_ds_bpermute(addr, int(uint32_t(v))));
-  const uint32_t hi = uint32_t(__builtin_amdgcn_ds_bpermute(addr, int(uint32_t(v >> 32))));
-  return uint64_t(lo) | (uint64_t(hi) << 32);
+// a m + c for signed 32-bit a, m and a 64-bit c, as one v_mad_i64_i32 (the
+// compiler expands a product by a power of two into a sign extension and
+// 64-bit shifts and adds, several instructions per term).  Its carry-out
+// lane mask is not read.
+__device__ __forceinline__ int64_t mad_i64(int a, int m, int64_t c) {
+  int64_t r;
+  uint64_t unused;
+  asm("v_mad_i64_i32 %0, %1, %2, %3, %4" : "=v"(r), "=s"(unused) : "v"(a), "s"(m), "v"(c));
+  return r;
 }
 
 // Tile (tm, tn) of this workgroup in the gridDim.y x gridDim.x tile grid.
@@ -686,10 +689,13 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(C
   for (int cb = 0; cb < CB; ++cb) {
     const int c2 = wn * 32 * CB + cb * 32 + i;
     const int col = n0 + c2;
-    if (col >= N) continue;  // the same for lanes l and l ^ 32
-    const int64_t s_n = int64_t(colsum[cb]) + __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, colsum[cb]);
+    // the two lane halves' sums of the column (lanes l and l ^ 32): after the
+    // swap one register holds lanes 0-31's values in both halves, the other
+    // lanes 32-63's
+    const auto cs = __builtin_amdgcn_permlane32_swap(colsum[cb], colsum[cb], false, false);
+    const int64_t s_n = int64_t(int(cs[0])) + int64_t(int(cs[1]));
     const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
-    const int sh = 8 * plane + (shifts ? int(shifts[col]) : 0);
+    const int sh = 8 * plane + (shifts && col < N ? int(shifts[col]) : 0);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       // register group g: share row g of the block, digits 4 khalf .. 4 khalf + 3
@@ -697,19 +703,29 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(C
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         // sum_ii acc_ii 256^ii fits 56 signed bits: three 32x32+64 MADs
-        const int64_t v = int64_t(acc[rb][cb][4 * g]) + int64_t(acc[rb][cb][4 * g + 1]) * 256 +
-                          int64_t(acc[rb][cb][4 * g + 2]) * 65536 + int64_t(acc[rb][cb][4 * g + 3]) * 16777216;
+        const int64_t v = mad_i64(acc[rb][cb][4 * g + 3], 16777216,
+                                  mad_i64(acc[rb][cb][4 * g + 2], 65536,
+                                          mad_i64(acc[rb][cb][4 * g + 1], 256, int64_t(acc[rb][cb][4 * g]))));
         part[g] = uint64_t(v) << (32 * khalf);
       }
-      // this half writes rows 2 khalf, 2 khalf + 1 and sends the other two
-      const uint64_t own0 = khalf ? part[2] : part[0], own1 = khalf ? part[3] : part[1];
-      const uint64_t give0 = khalf ? part[0] : part[2], give1 = khalf ? part[1] : part[3];
-      const uint64_t sum0 = own0 + swap_halves(give0, lane), sum1 = own1 + swap_halves(give1, lane);
+      // rows g and g + 2: lanes 0-31 write row g, lanes 32-63 row g + 2.  The
+      // swap moves lanes 32-63 of part[g] and lanes 0-31 of part[g + 2] across,
+      // after which every lane holds its own half's value and the other
+      // half's for the row it writes, one in each register
+      uint64_t sum[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const auto lo = __builtin_amdgcn_permlane32_swap(uint32_t(part[a]), uint32_t(part[a + 2]), false, false);
+        const auto hi =
+            __builtin_amdgcn_permlane32_swap(uint32_t(part[a] >> 32), uint32_t(part[a + 2] >> 32), false, false);
+        sum[a] = ((uint64_t(hi[0]) << 32) | lo[0]) + ((uint64_t(hi[1]) << 32) | lo[1]);
+      }
+      if (col >= N) continue;  // the same for lanes l and l ^ 32
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int row = m0 + wm * 16 + rb * 4 + 2 * khalf + a;
         if (row >= M) continue;
-        uint64_t v = corr + (a ? sum1 : sum0);
+        uint64_t v = corr + sum[a];
         v = sh < 64 ? (v << sh) : 0;
         if (split)
           atomicAdd(reinterpret_cast<unsigned long long*>(y + size_t(row) * N + col), (unsigned long long)v);
