@@ -480,8 +480,9 @@ struct HalfOps {
   v4i a[4], b[CB];
 };
 
-template <int CB, class RAW, class WT>
-__device__ __forceinline__ void read_half(const DmaCtx& c, int ks, const RAW& raw, const WT& wt, HalfOps<CB>& o) {
+template <int CB, int KS, class RAW, class WT>
+__device__ __forceinline__ void read_half(const DmaCtx& c, const RAW& raw, const WT& wt, HalfOps<CB>& o) {
+  constexpr int ks = KS;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) o.b[cb] = *reinterpret_cast<const v4i*>(&wt[c.w_off[ks] + 2048 * cb]);
 #pragma unroll
@@ -533,7 +534,7 @@ template <int CB, class RAWS, class WTS, class RAWN, class WTN>
 __device__ __forceinline__ void piped_step(const DmaCtx& c, int s, int steps, int k_begin, RAWS raw_s, WTS wt_s,
                                            RAWN raw_n, WTN wt_n, HalfOps<CB>& h0, HalfOps<CB>& h1,
                                            int (&colsum)[CB], v16i (&acc)[4][CB]) {
-  read_half<CB>(c, 1, raw_s, wt_s, h1);
+  read_half<CB, 1>(c, raw_s, wt_s, h1);
   mfma_half<CB>(h0, colsum, acc);
   interleave_half<CB>();
   // step s + 1's DMAs are done when only step s + 2's (4 + CB = 7) remain in
@@ -541,7 +542,7 @@ __device__ __forceinline__ void piped_step(const DmaCtx& c, int s, int steps, in
   // hold for every wave, so stage s may be refilled
   asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   dma_issue<CB>(c, k_begin + min(s + 3, steps - 1) * kBK, raw_s, wt_s);
-  read_half<CB>(c, 0, raw_n, wt_n, h0);
+  read_half<CB, 0>(c, raw_n, wt_n, h0);
   mfma_half<CB>(h1, colsum, acc);
   interleave_half<CB>();
 }
@@ -574,6 +575,53 @@ __device__ __forceinline__ void tile_of(int& tm, int& tn) {
   const int in = t - group * G * TN;
   tm = first + in % rows;
   tn = in / rows;
+}
+
+// Epilogue of one accumulator tile of a wave: rows row0 .. row0 + 3 (this lane
+// writes rows row0 + 2 khalf and row0 + 2 khalf + 1), column col.  The lane
+// holds, for its column, digits 4 khalf .. 4 khalf + 3 of the four rows in
+// register groups g (rows row0 + g); the halves of the wave add their digit
+// sums with v_permlane32_swap: swapping lanes 32-63 of part[g] with lanes 0-31
+// of part[g + 2] leaves every lane with its own half's value and the other
+// half's for the row it writes, one in each register.  corr is the
+// offset-binary correction of the column, sh its shift.
+__device__ __forceinline__ void store_tile(const v16i& a, int row0, int col, int khalf, uint64_t corr, int sh,
+                                           bool split, uint64_t mask, uint64_t* __restrict__ y, int M, int N) {
+  uint64_t part[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    // sum_ii acc_ii 256^ii fits 56 signed bits: three 32x32+64 MADs
+    const int64_t v = mad_i64(a[4 * g + 3], 16777216, mad_i64(a[4 * g + 2], 65536, mad_i64(a[4 * g + 1], 256, int64_t(a[4 * g]))));
+    part[g] = uint64_t(v) << (32 * khalf);
+  }
+  uint64_t sum[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const auto lo = __builtin_amdgcn_permlane32_swap(uint32_t(part[h]), uint32_t(part[h + 2]), false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(uint32_t(part[h] >> 32), uint32_t(part[h + 2] >> 32), false, false);
+    sum[h] = ((uint64_t(hi[0]) << 32) | lo[0]) + ((uint64_t(hi[1]) << 32) | lo[1]);
+  }
+  if (col >= N) return;  // the same for lanes l and l ^ 32
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = row0 + 2 * khalf + h;
+    if (row >= M) continue;
+    uint64_t v = corr + sum[h];
+    v = sh < 64 ? (v << sh) : 0;
+    if (split)
+      atomicAdd(reinterpret_cast<unsigned long long*>(y + size_t(row) * N + col), (unsigned long long)v);
+    else
+      y[size_t(row) * N + col] = v & mask;
+  }
+}
+
+// The offset-binary correction 0x8080808080808080 sum_k w[col][k] of a column
+// from this lane's column sum (lanes l and l ^ 32 hold the two halves of the
+// column's K chunks; after the swap one register holds lanes 0-31's values in
+// both halves, the other lanes 32-63's).
+__device__ __forceinline__ uint64_t column_correction(int colsum) {
+  const auto cs = __builtin_amdgcn_permlane32_swap(colsum, colsum, false, false);
+  return 0x8080808080808080ull * uint64_t(int64_t(int(cs[0])) + int64_t(int(cs[1])));
 }
 
 // Weight planes: w holds `planes` int8 matrices [planes][N][K], plane e the
@@ -662,7 +710,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(C
     dma_issue<CB>(c, k_begin + min(2, steps - 1) * kBK, raw2, wt2);
     asm volatile("s_waitcnt vmcnt(14)\n\ts_barrier" ::: "memory");
     HalfOps<CB> h0, h1;
-    read_half<CB>(c, 0, raw0, wt0, h0);
+    read_half<CB, 0>(c, raw0, wt0, h0);
     int q = 0;  // stage of step s
     for (int s = 0; s < steps; ++s) {
       const int qn = q == 2 ? 0 : q + 1;
@@ -684,55 +732,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(C
   const bool split = gridDim.z > 1;
 
   // ---- epilogue: column sums, digit recombination, shift, mask
-  const int i = c.i, khalf = c.khalf, wm = c.wm, wn = c.wn;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    const int c2 = wn * 32 * CB + cb * 32 + i;
-    const int col = n0 + c2;
-    // the two lane halves' sums of the column (lanes l and l ^ 32): after the
-    // swap one register holds lanes 0-31's values in both halves, the other
-    // lanes 32-63's
-    const auto cs = __builtin_amdgcn_permlane32_swap(colsum[cb], colsum[cb], false, false);
-    const int64_t s_n = int64_t(int(cs[0])) + int64_t(int(cs[1]));
-    const uint64_t corr = 0x8080808080808080ull * uint64_t(s_n);
+    const int col = n0 + c.wn * 32 * CB + cb * 32 + c.i;
+    const uint64_t corr = column_correction(colsum[cb]);
     const int sh = 8 * plane + (shifts && col < N ? int(shifts[col]) : 0);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      // register group g: share row g of the block, digits 4 khalf .. 4 khalf + 3
-      uint64_t part[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // sum_ii acc_ii 256^ii fits 56 signed bits: three 32x32+64 MADs
-        const int64_t v = mad_i64(acc[rb][cb][4 * g + 3], 16777216,
-                                  mad_i64(acc[rb][cb][4 * g + 2], 65536,
-                                          mad_i64(acc[rb][cb][4 * g + 1], 256, int64_t(acc[rb][cb][4 * g]))));
-        part[g] = uint64_t(v) << (32 * khalf);
-      }
-      // rows g and g + 2: lanes 0-31 write row g, lanes 32-63 row g + 2.  The
-      // swap moves lanes 32-63 of part[g] and lanes 0-31 of part[g + 2] across,
-      // after which every lane holds its own half's value and the other
-      // half's for the row it writes, one in each register
-      uint64_t sum[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const auto lo = __builtin_amdgcn_permlane32_swap(uint32_t(part[a]), uint32_t(part[a + 2]), false, false);
-        const auto hi =
-            __builtin_amdgcn_permlane32_swap(uint32_t(part[a] >> 32), uint32_t(part[a + 2] >> 32), false, false);
-        sum[a] = ((uint64_t(hi[0]) << 32) | lo[0]) + ((uint64_t(hi[1]) << 32) | lo[1]);
-      }
-      if (col >= N) continue;  // the same for lanes l and l ^ 32
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const int row = m0 + wm * 16 + rb * 4 + 2 * khalf + a;
-        if (row >= M) continue;
-        uint64_t v = corr + sum[a];
-        v = sh < 64 ? (v << sh) : 0;
-        if (split)
-          atomicAdd(reinterpret_cast<unsigned long long*>(y + size_t(row) * N + col), (unsigned long long)v);
-        else
-          y[size_t(row) * N + col] = v & mask;
-      }
-    }
+    for (int rb = 0; rb < 4; ++rb)
+      store_tile(acc[rb][cb], m0 + c.wm * 16 + rb * 4, col, c.khalf, corr, sh, split, mask, y, M, N);
   }
 }
 
