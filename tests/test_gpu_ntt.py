@@ -62,6 +62,37 @@ def test_ntt_all_sizes(gpu, log_n):
     _roundtrip_case(q, log_n, 6, 0x77 + log_n, gpu, patterns=False)
 
 
+@pytest.mark.parametrize("log_n,limbs", [(11, 4096), (12, 3072), (13, 1536)])
+def test_ntt_many_limbs_per_workgroup(gpu, log_n, limbs):
+    """More limbs than resident workgroups, so that each workgroup runs the
+    persistent loop several times (the next limb's loads issued before the
+    current limb's last pass or stores): the first and last limbs against the
+    oracle, forward and inverse, and the round trip on every limb."""
+    import torch
+    n = 1 << log_n
+    q = [cf.primes_below(50, n, 1)[0], cf.primes_below(49, n, 1)[0], cf.primes_below(60, n, 1)[0]]
+    print(f"[ntt] log_n={log_n} limbs={limbs} (persistent loop)", flush=True)
+    a = oracle.fill_residues(limbs, n, q, 0x5052414700000300 + log_n)
+    tab = oracle.Tables(q, log_n)
+    plan = praghip.NttBatch(q, log_n)
+    t = to_dev(a)
+    plan.forward(t)
+    fwd = from_dev(t)
+    # the oracle takes limb l of its input to prime l % P: slices start at a
+    # multiple of P
+    tail = (limbs - 48) // len(q) * len(q)
+    np.testing.assert_array_equal(fwd[:48], oracle.ntt(a[:48], tab))
+    np.testing.assert_array_equal(fwd[tail:], oracle.ntt(a[tail:], tab))
+    plan.inverse(t)
+    assert torch.equal(t, to_dev(a))
+    b = oracle.fill_residues(limbs, n, q, 0x5052414700000310 + log_n)
+    tb = to_dev(b)
+    plan.inverse(tb)
+    inv = from_dev(tb)
+    np.testing.assert_array_equal(inv[:48], oracle.ntt(b[:48], tab, inverse=True))
+    np.testing.assert_array_equal(inv[tail:], oracle.ntt(b[tail:], tab, inverse=True))
+
+
 def test_ntt_golden_small(gpu, golden_dir):
     data = np.load(os.path.join(golden_dir, "ntt_small.npz"))
     names = sorted({k.rsplit("_", 1)[0] for k in data.files})
