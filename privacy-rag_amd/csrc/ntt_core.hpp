@@ -216,7 +216,7 @@ struct ArU64LC : ArU64L {
 //             the last stage multiplies both outputs (N^-1 folded).
 struct ArF64 {
   using T = double;
-  using TW = double;  // w; w/q is formed in registers
+  using TW = double;  // w (the quotient is estimated from the rounded product)
   static constexpr bool kAhead = true;  // load the next pass's twiddles one pass early
   double q, qinv;
   __device__ explicit ArF64(const NttPrime& p) : q(p.qd), qinv(p.qinv) {}
@@ -232,7 +232,7 @@ struct ArF64 {
   }
   __device__ __forceinline__ uint64_t to_u64_fwd(T x) const { return to_u64(x); }
   __device__ __forceinline__ uint64_t to_u64_inv(T x) const { return to_u64(x); }
-  __device__ __forceinline__ T mul(T a, TW w) const { return mul_f64(a, w, w * qinv, q); }
+  __device__ __forceinline__ T mul(T a, TW w) const { return mul_f64_hq(a, w, q, qinv); }
   template <bool = false>
   __device__ __forceinline__ void fwd(T& x, T& y, TW w) const {
     const T t = mul(y, w);

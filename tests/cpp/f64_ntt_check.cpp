@@ -1,5 +1,5 @@
 // CPU check of the float-path NTT arithmetic (ArF64 in ntt_core.hpp with
-// mul_f64 / reduce_f64 from modarith.hpp), stage by stage in the reference's
+// mul_f64_hq / reduce_f64 from modarith.hpp), stage by stage in the reference's
 // radix-2 order (ntt.cu:42-53).  The register passes of the GPU kernel apply
 // the same butterflies to the same operands and re-centre whole blocks after
 // the same stages, so every intermediate value here equals the GPU's.
@@ -42,7 +42,7 @@ struct Checker {
   double mul(double a, double w, uint64_t wi, uint64_t ai) {
     max_factor = std::fmax(max_factor, std::fabs(a) / qd);
     if (std::fabs(a) > factor_lim * qd) ++bad;
-    const double r = mul_f64(a, w, w * qinv, qd);
+    const double r = mul_f64_hq(a, w, qd, qinv);  // ArF64::mul
     if (res(r) != mulmod(ai, wi, q)) ++bad;
     return r;
   }
