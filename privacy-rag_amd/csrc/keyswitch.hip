@@ -221,6 +221,7 @@ __device__ __forceinline__ void ks_item_f64(const KsFused& f, const KsConst& kc,
     ntt_regs<LOGN, false>(e, xl, th, f.tw_fwd_f + (size_t(t) << LOGN), ar, pr);
     const uint64_t* k0 = kb + ((size_t(j) * 2 * K) << LOGN);
     const uint64_t* k1 = k0 + (size_t(K) << LOGN);
+    const bool settle = (j & 3) == 3 || j + 1 == dnum;
 #pragma unroll
     for (int r = 0; r < kE; r += 2) {
       // registers r and r + 1 sit at adjacent positions after the last
@@ -232,12 +233,19 @@ __device__ __forceinline__ void ks_item_f64(const KsFused& f, const KsConst& kc,
       for (int h = 0; h < 2; ++h) {
         const int rr = r + h;
         const unsigned si = unsigned(rr) * TH + th;
-        // |e| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
+        // |e| <= 3.44 q after the last forward stage: products |p| <= 1.8 q,
+        // summed without re-centring and re-centred after every fourth
+        // digit and after the last, so the sums stay within
+        // q/2 + 1 + 4 (1.8 q) < 8 q < 2^53
         const double p0 = ar.mul(e[rr], ArF64::from_u64(h ? ka.y : ka.x));
         double p1 = ar.mul(e[rr], ArF64::from_u64(h ? kb.y : kb.x));
-        acc0[rr] = reduce_f64(j ? acc0[rr] + p0 : p0, ar.q, ar.qinv);
+        acc0[rr] = j ? acc0[rr] + p0 : p0;
         if (j) p1 += as_f64(s1[si]);
-        s1[si] = as_u64(reduce_f64(p1, ar.q, ar.qinv));
+        if (settle) {
+          acc0[rr] = reduce_f64(acc0[rr], ar.q, ar.qinv);
+          p1 = reduce_f64(p1, ar.q, ar.qinv);
+        }
+        s1[si] = as_u64(p1);
       }
       if ((r & 3) == 2) __builtin_amdgcn_sched_barrier(0);
     }

@@ -533,7 +533,7 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
   for (int k = 0; k < E; ++k) en[k] = __builtin_nontemporal_load(&e0[fwd_in_index<kRowLog, kRowLE>(t2, k)]);
   __syncthreads();
   T a0[E], a1[E];
-  if constexpr (kMont) {
+  if constexpr (kMont || kF64) {
 #pragma unroll
     for (int k = 0; k < E; ++k) a0[k] = a1[k] = 0;
   }
@@ -575,11 +575,12 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
         const int rr = r + h;
         const uint64_t w0 = h ? ka.y : ka.x, w1 = h ? kk.y : kk.x;
         if constexpr (kF64) {
-          // |v| <= 3.44 q after the last forward stage: products |p| <= 1.8 q
-          const double p0 = ar.mul(v[rr], ArF64::from_u64(w0));
-          const double p1 = ar.mul(v[rr], ArF64::from_u64(w1));
-          a0[rr] = reduce_f64(j ? a0[rr] + p0 : p0, ar.q, ar.qinv);
-          a1[rr] = reduce_f64(j ? a1[rr] + p1 : p1, ar.q, ar.qinv);
+          // |v| <= 3.44 q after the last forward stage: products |p| <= 1.8 q,
+          // added from zero without re-centring; the sums are re-centred
+          // after every fourth digit and after the last, so they stay within
+          // q/2 + 1 + 4 (1.8 q) < 8 q < 2^53
+          a0[rr] += ar.mul(v[rr], ArF64::from_u64(w0));
+          a1[rr] += ar.mul(v[rr], ArF64::from_u64(w1));
         } else if constexpr (kMont) {
           // x < 12q after stage 13, canonical key words: each product < 2q
           a0[rr] += mul_mont(v[rr], w0, ar.q, kc.neg_qinv[t]);
@@ -601,9 +602,24 @@ __device__ __forceinline__ void row_item2(const KsRows& f, const KsConst& kc, un
           a1[k] = a1[k] >= ar.q8 ? a1[k] - ar.q8 : a1[k];
         }
       }
+    } else if constexpr (kF64) {
+      if ((j & 3) == 3) {
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+          a0[k] = reduce_f64(a0[k], ar.q, ar.qinv);
+          a1[k] = reduce_f64(a1[k], ar.q, ar.qinv);
+        }
+      }
     }
     // the next digit's first exchange writes the LDS this digit's last one
     // read, and crosses the waves: it starts with a workgroup barrier
+  }
+  if constexpr (kF64) {  // re-centred, |x| <= q/2 + 1: the inverse passes' input bound
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      a0[k] = reduce_f64(a0[k], ar.q, ar.qinv);
+      a1[k] = reduce_f64(a1[k], ar.q, ar.qinv);
+    }
   }
   if constexpr (kMont) {  // below 16q -> below 4q, the lazy inverse's input bound
 #pragma unroll
