@@ -1,8 +1,10 @@
 // CPU check of the integer helpers in modarith.hpp against 128-bit host
 // arithmetic: shoup_quotient(w, m) == floor(w 2^64 / q) and mul_shoup /
 // mul_barrett == a w mod q, for primes from 2^20 to 2^62 and edge operands
-// (0, 1, q-1, q/2, random), and mul_mont (x k 2^-64 mod q) for primes below
-// 2^60.  Plants a wrong ratio and a wrong -q^-1 to show the checks fail.
+// (0, 1, q-1, q/2, random), mul_mont (x k 2^-64 mod q) for primes below
+// 2^60, and the float product mul_f64_hq against its bound for primes below
+// 2^50.  Plants a wrong ratio, a wrong -q^-1 and a wrong reciprocal to show
+// the checks fail.
 #include <cstdio>
 #include <random>
 #include <vector>
@@ -49,6 +51,34 @@ static int check_mont(uint64_t q, uint64_t nq, std::mt19937_64& rng) {
   return bad;
 }
 
+// mul_f64_hq (the float path's product, q < 2^50): for |a| <= A q and w < q
+// the result r is an integer with r == a w (mod q) and |r| <= (1/2 + 3A/8) q
+// (the bound the re-centring schedules rely on), for A up to 8.  qinv is
+// `qinv` (1/q rounded, or a planted wrong value).
+static int check_f64(uint64_t q, double qinv, std::mt19937_64& rng) {
+  int bad = 0;
+  const double qd = double(q);
+  std::vector<uint64_t> ws = {0, 1, q - 1, q / 2, q - 2};
+  for (int i = 0; i < 300; ++i) ws.push_back(rng() % q);
+  for (double A : {1.0, 4.0, 5.3, 7.7, 8.0}) {
+    const int64_t amax = int64_t(A * qd);
+    std::vector<int64_t> as = {0, 1, -1, amax, -amax, amax - 1, int64_t(q) - 1};
+    for (int i = 0; i < 300; ++i) as.push_back(int64_t(rng() % uint64_t(2 * amax + 1)) - amax);
+    const double lim = (0.5 + 0.375 * A) * qd;
+    for (int64_t a : as)
+      for (uint64_t w : ws) {
+        const double r = mul_f64_hq(double(a), double(w), qd, qinv);
+        if (r != __builtin_rint(r) || __builtin_fabs(r) > lim) {
+          ++bad;
+          continue;
+        }
+        const __int128 d = (__int128)a * (__int128)w - (__int128)(int64_t)r;
+        if (d % (__int128)q != 0) ++bad;
+      }
+  }
+  return bad;
+}
+
 int main() {
   std::mt19937_64 rng(12345);
   const std::vector<uint64_t> primes = {
@@ -75,8 +105,15 @@ int main() {
     mont_bad += check_mont(q, nq, rng);
     mont_planted += check_mont(q, nq + 2, rng) > 0;
   }
-  printf("bad=%d planted=%d mont_bad=%d mont_planted=%d\n", bad, planted, mont_bad, mont_planted);
-  const bool ok = bad == 0 && planted > 0 && mont_bad == 0 && mont_planted == 4;
+  // the float product on primes below 2^50; a reciprocal 2^-30 too large
+  // must break the bound
+  int f64_bad = 0;
+  for (uint64_t q : {1048583ull, 1125899906826241ull, 562949952798721ull, 1125899904679937ull})
+    f64_bad += check_f64(q, 1.0 / double(q), rng);
+  const int f64_planted = check_f64(1125899906826241ull, (1.0 / 1125899906826241.0) * (1.0 + 0x1p-30), rng);
+  printf("bad=%d planted=%d mont_bad=%d mont_planted=%d f64_bad=%d f64_planted=%d\n", bad, planted, mont_bad,
+         mont_planted, f64_bad, f64_planted);
+  const bool ok = bad == 0 && planted > 0 && mont_bad == 0 && mont_planted == 4 && f64_bad == 0 && f64_planted > 0;
   printf(ok ? "ALL OK\n" : "FAIL\n");
   return !ok;
 }

@@ -1,5 +1,5 @@
 """Host-side check of the float-path NTT arithmetic (q < 2^50): the device
-code's mul_f64 / reduce_f64 and re-centring schedule, run stage by stage on
+code's mul_f64_hq / reduce_f64 and re-centring schedule, run stage by stage on
 the CPU, keep every intermediate an exact integer congruent to the true
 residue, every product factor within 4q and every value below 2^53, and the
 outputs equal the oracle's transform (which is pinned by the closed form)."""
@@ -55,10 +55,11 @@ def test_float_path_exact_and_bounded():
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="no hipcc")
 def test_integer_helpers_exact():
-    """shoup_quotient, mul_shoup and mul_barrett of modarith.hpp against 128-bit host arithmetic."""
+    """shoup_quotient, mul_shoup, mul_barrett, mul_mont and mul_f64_hq of modarith.hpp against
+    128-bit host arithmetic (and the float product against its bound)."""
     with tempfile.TemporaryDirectory() as d:
         exe = os.path.join(d, "modarith_check")
-        subprocess.run([HIPCC, "-O2", "-std=c++17", "-x", "hip", "--offload-arch=gfx950",
+        subprocess.run([HIPCC, "-O2", "-std=c++17", "-x", "hip", "--offload-arch=gfx950", "-ffp-contract=off",
                         "-I", os.path.join(ROOT, "privacy-rag_amd", "csrc"),
                         os.path.join(ROOT, "tests", "cpp", "modarith_check.cpp"), "-o", exe],
                        check=True, capture_output=True)
