@@ -26,6 +26,11 @@ def _roundtrip_case(q, log_n, limbs, seed, gpu, patterns=True):
         a[0, j % 13 == 0] = 0
         a[0, j % 13 == 1] = qq - np.uint64(1)
         a[0, j % 13 == 2] = 1
+        # the largest growth of the lazy float path: every word q - 1, and
+        # q - 1 / 0 alternating (limb l uses prime l % len(q))
+        if limbs > 2:
+            a[1, :] = np.uint64(q[1 % len(q)]) - np.uint64(1)
+            a[2, :] = np.where(j % 2 == 0, np.uint64(q[2 % len(q)]) - np.uint64(1), np.uint64(0))
     tab = oracle.Tables(q, log_n)
     plan = praghip.NttBatch(q, log_n, device=0)
     t = to_dev(a)
