@@ -78,6 +78,22 @@ def test_keyswitch_edge_inputs(gpu):
         np.testing.assert_array_equal(sw.apply(ct), want, err_msg=name)
 
 
+@pytest.mark.parametrize("dnum", [3, 6])
+def test_keyswitch_max_key_words(gpu, dnum):
+    """Every key word q_t - 1 and every ciphertext word q_i - 1: the largest key
+    products, whose sums over the digits the float items add without
+    re-centring (dnum = 6: six one-prime digits, re-centred after the fourth)."""
+    q, n, L = P16384_SWITCH, 16384, 6
+    print(f"[ks] max key words dnum={dnum}", flush=True)
+    qk = np.array(q, dtype=np.uint64)[None, None, :, None]
+    key = np.broadcast_to(qk - np.uint64(1), (dnum, 2, L + 1, n)).copy()
+    sw = praghip.Switch(q, 14, dnum, key=key)
+    qs = np.array(q[:L], dtype=np.uint64)[:, None]
+    ct = np.broadcast_to(qs - np.uint64(1), (2, L, n)).copy()
+    want = oracle.keyswitch(ct[None], key, q, dnum, 14, 1)[0]
+    np.testing.assert_array_equal(sw.apply(ct), want)
+
+
 def test_switch_errors_and_cleanup(gpu):
     q, n, L, dnum = cf.LOCKED_PRIMES, 16384, 6, 6
     key = oracle.fill_residues(dnum * 2 * (L + 1), n, q, 1).reshape(dnum, 2, L + 1, n)
